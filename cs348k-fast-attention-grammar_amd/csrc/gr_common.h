@@ -1,0 +1,91 @@
+// gr_common.h -- device-side vocabulary shared by the hand-written CDNA4 kernels
+// and by every HIP translation unit the grammar renderer emits (hiprtc includes
+// this file by name). gfx950 only: 64-lane wavefronts, the double-K MFMA family
+// (v_mfma_f32_32x32x16_{f16,bf16}), 160 KiB of LDS per CU.
+//
+// Self-contained on purpose: hiprtc compiles it without the C++ standard
+// library, so nothing here includes a system header beyond what hiprtc provides.
+#pragma once
+
+#ifndef GR_INF
+#define GR_INF __builtin_inff()
+#endif
+
+typedef _Float16 gr_f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 gr_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 gr_f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 gr_bf16x4 __attribute__((ext_vector_type(4)));
+typedef float gr_f32x16 __attribute__((ext_vector_type(16)));
+typedef float gr_f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int gr_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int gr_u32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// Element traits: storage type T (fp16 or bf16) -> MFMA operand vector and the
+// 32x32x16 matrix-core op. Operand layout (A: M x K, B: K x N, lane l):
+//   A[m][k]: m = l % 32, k in the 8-wide group (l / 32)
+//   B[k][n]: n = l % 32, k in the 8-wide group (l / 32)
+//   D[m][n]: n = l % 32, m = 8*(r/4) + 4*(l/32) + (r%4) for accumulator r
+// Only the pairing of k between A and B matters for a contraction, so callers
+// may assign any 8 contraction indices to a lane group as long as A and B agree.
+// ---------------------------------------------------------------------------
+template <class T> struct gr_mfma;
+
+template <> struct gr_mfma<_Float16> {
+  typedef gr_f16x8 vec8;
+  typedef gr_f16x4 vec4;
+  static __device__ __forceinline__ gr_f32x16 mma32(vec8 a, vec8 b, gr_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ gr_f32x4 mma16(vec8 a, vec8 b, gr_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <> struct gr_mfma<__bf16> {
+  typedef gr_bf16x8 vec8;
+  typedef gr_bf16x4 vec4;
+  static __device__ __forceinline__ gr_f32x16 mma32(vec8 a, vec8 b, gr_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ gr_f32x4 mma16(vec8 a, vec8 b, gr_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+// 16-byte and 8-byte raw moves. The bit casts keep the vector registers intact.
+template <class V>
+__device__ __forceinline__ V gr_as(gr_u32x4 x) { return __builtin_bit_cast(V, x); }
+template <class V>
+__device__ __forceinline__ gr_u32x4 gr_raw(V x) { return __builtin_bit_cast(gr_u32x4, x); }
+
+__device__ __forceinline__ gr_u32x4 gr_ld16(const void* p) {
+  return *reinterpret_cast<const gr_u32x4*>(p);
+}
+__device__ __forceinline__ void gr_st16(void* p, gr_u32x4 v) {
+  *reinterpret_cast<gr_u32x4*>(p) = v;
+}
+
+// Exchange with the lane 32 positions away (the other half of the wavefront).
+__device__ __forceinline__ float gr_xor32(float v) {
+  return __shfl_xor(v, 32, 64);
+}
+
+// 2^x on the transcendental unit (v_exp_f32). Inputs here are <= 0 or -inf.
+__device__ __forceinline__ float gr_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Pack two storage-type values into one dword (low = a, high = b).
+template <class T>
+__device__ __forceinline__ unsigned int gr_pack2(T a, T b) {
+  unsigned short lo = __builtin_bit_cast(unsigned short, a);
+  unsigned short hi = __builtin_bit_cast(unsigned short, b);
+  return (unsigned int)lo | ((unsigned int)hi << 16);
+}
+
+// Workgroup index remap so that consecutive logical blocks land on the same
+// XCD (MI355X dispatches workgroups round-robin over its 8 XCDs, each with its
+// own L2). Blocks that share K/V (same head) then share an L2.
+__device__ __forceinline__ int gr_xcd_remap(int bid, int nblk) {
+  if ((nblk & 7) != 0) return bid;
+  return (bid & 7) * (nblk >> 3) + (bid >> 3);
+}

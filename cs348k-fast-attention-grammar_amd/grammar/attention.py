@@ -1,0 +1,87 @@
+"""Python face of the hand-written CDNA4 attention forward (gr_attn_fwd).
+
+`flash_attention_fwd(q, k, v)` computes softmax(scale * q k^T [causal]) v for
+[B, H, N, D] fp16/bf16 tensors on the GPU -- the same math as the reference's
+attention module contract `fn(KT, Q, V)` (pytorch-naive.py:23-65,
+run_attention_search.py:169-181) and its SDPA reference point
+(flash-attn2-sota.py:41-62), batched over B and H.
+
+There is no CPU path: CPU tensors or a missing library raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+from . import runtime as rt
+
+
+def _strides3(t, dims=(0, 1, 2)) -> "ctypes.Array":
+    return rt._ll3(*(int(t.stride(d)) for d in dims))
+
+
+def flash_attention_fwd(q, k, v, *, causal: bool = False, scale: float | None = None,
+                        k_transposed: bool = False, block_m: int = 0, block_n: int = 0,
+                        out=None, stream=None):
+    """O = softmax(scale * Q K^T [+ causal mask]) V on the MI355X.
+
+    q, v: [B, H, N, D]; k: [B, H, N, D], or [B, H, D, N] when k_transposed.
+    All three share dtype (float16 or bfloat16) and live on the GPU. Returns a
+    new [B, H, N, D] tensor (or writes `out`)."""
+    import torch
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not t.is_cuda:
+            raise ValueError(f"flash_attention_fwd: {name} must be a GPU tensor (no CPU path)")
+        if t.dtype != q.dtype:
+            raise ValueError("flash_attention_fwd: q, k, v must share a dtype")
+        if t.dim() != 4:
+            raise ValueError(f"flash_attention_fwd: {name} must be 4-D")
+    B, H, N, D = q.shape
+    if tuple(v.shape) != (B, H, N, D):
+        raise ValueError(f"flash_attention_fwd: v shape {tuple(v.shape)} != q shape {tuple(q.shape)}")
+    want_k = (B, H, D, N) if k_transposed else (B, H, N, D)
+    if tuple(k.shape) != want_k:
+        raise ValueError(f"flash_attention_fwd: k shape {tuple(k.shape)} != {want_k}")
+    if q.stride(3) != 1 or v.stride(3) != 1 or k.stride(3) != 1:
+        raise ValueError("flash_attention_fwd: innermost dimension must be contiguous")
+    if out is None:
+        out = torch.empty((B, H, N, D), dtype=q.dtype, device=q.device)
+    elif tuple(out.shape) != (B, H, N, D) or out.dtype != q.dtype or out.stride(3) != 1:
+        raise ValueError("flash_attention_fwd: bad `out` tensor")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    rc = rt.lib().gr_attn_fwd(
+        ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
+        ctypes.c_void_p(out.data_ptr()), rt.dtype_code(q.dtype), B, H, N, D,
+        _strides3(q), _strides3(k), _strides3(v), _strides3(out),
+        int(bool(k_transposed)), int(bool(causal)), float(scale), int(block_m), int(block_n),
+        rt._stream_ptr(stream))
+    rt.check(rc, "gr_attn_fwd")
+    return out
+
+
+def attention_flops(B: int, H: int, N: int, D: int, causal: bool = False) -> int:
+    """Algorithmic FLOPs of attention forward: 4*B*H*N^2*D (two GEMMs), halved
+    for a causal mask (old/benchmark.py:354-355 defines the 4*B*H*S^2*D count)."""
+    f = 4 * B * H * N * N * D
+    return f // 2 if causal else f
+
+
+def attention_io_bytes(B: int, H: int, N: int, D: int, elem_bytes: int = 2) -> int:
+    """Minimal HBM traffic: read Q, K, V once and write O once."""
+    return 4 * B * H * N * D * elem_bytes
+
+
+def mfma32_selftest(a, b):
+    """D = A[32,16] @ B[16,32] through one 32x32x16 MFMA with the operand and
+    accumulator layout the kernels assume (fp16 in, fp32 out)."""
+    import torch
+    if a.shape != (32, 16) or b.shape != (16, 32) or a.dtype != torch.float16 or b.dtype != torch.float16:
+        raise ValueError("mfma32_selftest: need fp16 A[32,16] and B[16,32]")
+    a = a.contiguous()
+    b = b.contiguous()
+    d = torch.empty((32, 32), dtype=torch.float32, device=a.device)
+    rt.check(rt.lib().gr_selftest_mfma32(ctypes.c_void_p(a.data_ptr()), ctypes.c_void_p(b.data_ptr()),
+                                         ctypes.c_void_p(d.data_ptr()), rt._stream_ptr(None)),
+             "gr_selftest_mfma32")
+    return d

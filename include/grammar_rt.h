@@ -1,0 +1,124 @@
+/* grammar_rt.h -- C ABI of libgrammar_rt.so, the MI355X (gfx950) runtime of
+ * the kernel-grammar descent.
+ *
+ * The reference has no native library: its generated modules are cuTile
+ * Python, JIT-compiled by cuda.tile and launched/timed through cupy. Every
+ * entry point below replaces one piece of that Python/vendor boundary; the
+ * comment on each names the reference site it stands in for.
+ *
+ * Conventions
+ *  - Plain C types only. Device buffers are raw pointers owned by the caller
+ *    (PyTorch-ROCm tensors in the Python layer); the library never frees them.
+ *  - Every function returns 0 on success or a negative GR_E* code; the
+ *    message of the last failure on the calling thread is gr_last_error().
+ *  - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ */
+#ifndef GRAMMAR_RT_H
+#define GRAMMAR_RT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define GR_OK 0
+#define GR_E_ARG -1       /* invalid argument / unsupported shape */
+#define GR_E_COMPILE -2   /* hiprtc compilation failed */
+#define GR_E_LOAD -3      /* code object could not be loaded */
+#define GR_E_LAUNCH -4    /* kernel launch failed */
+#define GR_E_RUNTIME -5   /* any other HIP runtime error */
+
+/* ---- element types ----------------------------------------------------- */
+#define GR_F32 0
+#define GR_F16 1
+#define GR_BF16 2
+
+/* Message describing the last failure on this thread ("" if none). */
+const char* gr_last_error(void);
+
+/* Library / toolchain identification, e.g. "gfx950 hiprtc 7.2". The string is
+ * part of every on-disk code-object cache key. */
+const char* gr_version(void);
+
+/* ---- device properties -------------------------------------------------- */
+/* Fills: [0] CU count, [1] max LDS bytes per workgroup, [2] wavefront size,
+ * [3] peak engine clock kHz, [4] L2 bytes. For the roofline constants. */
+int gr_device_info(int device, long long* out5);
+
+/* ---- compilation (replaces the cuTile JIT: grammar/optimization.py:262-283,
+ *      grammar/kernel_ast.py:1228-1229) ------------------------------------ */
+
+/* Compile HIP C++ source `src` with hiprtc for gfx950. Options are passed
+ * through (include paths, -D...). On success *code/*code_size receive a
+ * malloc'd code object (free with gr_free_code). On a compile error the hiprtc
+ * log is copied to `log` (truncated to loglen) and GR_E_COMPILE is returned.
+ * Thread-safe: independent programs may be compiled concurrently. No HIP
+ * device context is touched. */
+int gr_compile(const char* src, const char* name, const char* const* opts, int nopts,
+               void** code, size_t* code_size, char* log, size_t loglen);
+void gr_free_code(void* code);
+
+typedef struct gr_module gr_module;
+typedef struct gr_kernel gr_kernel;
+
+/* Load a code object (from gr_compile or the on-disk cache). */
+int gr_module_load(const void* code, size_t code_size, gr_module** out);
+void gr_module_free(gr_module* mod);
+/* Look up an extern "C" __global__ function by name. The handle lives as long
+ * as its module. */
+int gr_get_kernel(gr_module* mod, const char* name, gr_kernel** out);
+
+/* ---- launch (replaces ct.launch: grammar/kernel_ast.py:1273-1275) -------- */
+
+/* Launch with every kernel parameter a 64-bit value (device pointers; the
+ * renderer bakes every shape into the source). */
+int gr_launch(gr_kernel* k, const uint32_t grid[3], const uint32_t block[3], uint32_t lds_bytes,
+              void* stream, const uint64_t* args, int nargs);
+
+/* A launch plan: the ordered stage launches of one generated module with
+ * their arguments bound (the reference's host fn(*inputs),
+ * grammar/kernel_ast.py:1267-1278, minus its per-call cp.zeros allocations:
+ * intermediates are allocated once by the caller). */
+typedef struct gr_plan gr_plan;
+int gr_plan_create(int nsteps, gr_plan** out);
+int gr_plan_set_step(gr_plan* p, int i, gr_kernel* k, const uint32_t grid[3], const uint32_t block[3],
+                     uint32_t lds_bytes, const uint64_t* args, int nargs);
+int gr_plan_run(gr_plan* p, void* stream);
+void gr_plan_free(gr_plan* p);
+
+/* ---- timing (replaces cp.cuda.Event timing: grammar/optimization.py:284-300,
+ *      bench.py:49-74) ------------------------------------------------------ */
+#define GR_TIME_BATCH 0   /* one event pair around `iters` back-to-back runs; mean ms */
+#define GR_TIME_MIN 1     /* one event pair per run; minimum ms over `iters` */
+int gr_plan_time(gr_plan* p, void* stream, int warmup, int iters, int mode, float* ms_out);
+
+/* ---- hand-written CDNA4 baselines -------------------------------------- */
+
+/* Flash-style attention forward, O = softmax(scale*Q K^T [causal]) V.
+ * Replaces the attention module contract fn(KT, Q, V) (bench.py:14-20,
+ * pytorch-naive.py:23-65, grammar/kernel_ast.py:1267-1287) and the SDPA
+ * reference point (flash-attn2-sota.py:41-62).
+ *  dtype: GR_F16 or GR_BF16 (fp32 accumulate).
+ *  Q, V, O: [B, H, N, D] with strides {batch, head, seq} in elements
+ *  (unit stride along D). K: [B, H, N, D] if k_transposed == 0, else KT
+ *  [B, H, D, N] whose k_strides = {batch, head, d} (unit stride along N).
+ *  D in {64, 128}; N a multiple of block_m and block_n.
+ *  block_m: queries per workgroup (0 = default), block_n: keys per tile
+ *  (0 = default). */
+int gr_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H,
+                int N, int D, const long long* q_strides, const long long* k_strides,
+                const long long* v_strides, const long long* o_strides, int k_transposed,
+                int causal, float scale, int block_m, int block_n, void* stream);
+
+/* Self-test of the 32x32x16 MFMA operand/accumulator layout the kernels
+ * assume: one wavefront computes D[32][32] = A[32][16] @ B[16][32] (fp16 in,
+ * fp32 out, all row-major device buffers). */
+int gr_selftest_mfma32(const void* a, const void* b, float* d, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GRAMMAR_RT_H */

@@ -1,0 +1,150 @@
+"""GPU parity of the hand-written CDNA4 attention forward (gr_attn_fwd) against
+the fp32 CPU oracle, on the same seeded inputs.
+
+Bar: max-abs <= 2e-2 and mean-abs <= 2e-3 against
+softmax(QK^T/sqrt(d))V computed in fp32 on the CPU from the fp16/bf16-rounded
+inputs. Full-size configs add size-independent properties (finiteness,
+convex hull of V, bitwise layout/stride invariance, determinism)."""
+import numpy as np
+import pytest
+
+from oracle import attention as O
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _cuda():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def _run(q, k, v, **kw):
+    from grammar.attention import flash_attention_fwd
+    o = flash_attention_fwd(q, k, v, **kw)
+    torch.cuda.synchronize()
+    return o
+
+
+def _check(o_gpu, ref, label):
+    got = o_gpu.float().cpu().numpy()
+    mx, mn = O.errors(got, ref)
+    print(f"[parity] {label}: max-abs {mx:.3e} mean-abs {mn:.3e}", flush=True)
+    assert np.isfinite(got).all(), label
+    assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL, (label, mx, mn)
+    return mx, mn
+
+
+def test_mfma32_layout_selftest():
+    dev = _cuda()
+    from grammar.attention import mfma32_selftest
+    g = torch.Generator("cpu").manual_seed(3)
+    a = torch.randn(32, 16, generator=g).half()
+    b = torch.randn(16, 32, generator=g).half()
+    d = mfma32_selftest(a.to(dev), b.to(dev)).cpu()
+    ref = a.double() @ b.double()
+    assert torch.allclose(d.double(), ref, atol=1e-3, rtol=1e-3), (d - ref).abs().max()
+
+
+SMALL = [
+    # B, H, N, D, dtype, causal, k_transposed, block_m, block_n
+    (1, 2, 256, 64, "fp16", False, False, 128, 64),
+    (1, 2, 256, 64, "bf16", False, False, 128, 64),
+    (1, 2, 256, 64, "fp16", True, False, 128, 64),
+    (1, 2, 256, 64, "fp16", False, True, 128, 64),
+    (1, 2, 256, 64, "bf16", True, True, 128, 64),
+    (2, 3, 256, 128, "fp16", False, False, 128, 64),
+    (2, 3, 256, 128, "bf16", True, False, 128, 64),
+    (1, 2, 512, 64, "fp16", False, False, 128, 32),
+    (1, 2, 512, 64, "fp16", True, False, 128, 128),
+    (1, 2, 512, 64, "fp16", False, False, 64, 64),
+    (1, 2, 512, 64, "fp16", True, False, 256, 64),
+    (1, 2, 512, 64, "bf16", False, True, 256, 32),
+    (1, 2, 512, 128, "bf16", True, True, 128, 32),
+    (1, 1, 128, 64, "fp16", True, False, 128, 64),
+]
+
+
+@pytest.mark.parametrize("case", SMALL, ids=lambda c: "-".join(map(str, c)))
+def test_attention_small_parity(case):
+    dev = _cuda()
+    from grammar.workloads import AttnConfig, attention_inputs
+    B, H, N, D, dt, causal, kt, bm, bn = case
+    cfg = AttnConfig("t", B, H, N, D, dt, causal)
+    q, k, v = attention_inputs(cfg, seed=11, k_transposed=kt)
+    ref = O.attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), causal=causal, k_transposed=kt)
+    o = _run(q.to(dev), k.to(dev), v.to(dev), causal=causal, k_transposed=kt, block_m=bm, block_n=bn)
+    _check(o, ref, str(case))
+
+
+def test_c1_shape_fp16():
+    # C1 is the CPU plumbing config (fp32); its shape runs on the GPU in fp16.
+    dev = _cuda()
+    from grammar.workloads import C1, attention_inputs
+    q, k, v = attention_inputs(C1, seed=0, dtype="fp16")
+    ref = O.attention(q.float().numpy(), k.float().numpy(), v.float().numpy())
+    _check(_run(q.to(dev), k.to(dev), v.to(dev)), ref, "C1@fp16")
+
+
+def test_c2_full_parity_and_layout_invariance():
+    dev = _cuda()
+    from grammar.workloads import C2, attention_inputs
+    q, k, v = attention_inputs(C2, seed=0)
+    ref = O.attention(q.float().numpy(), k.float().numpy(), v.float().numpy())
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    o = _run(qd, kd, vd)
+    _check(o, ref, "C2")
+    # KT layout stages the same LDS tile -> bitwise identical output.
+    o_kt = _run(qd, kd.transpose(-1, -2).contiguous(), vd, k_transposed=True)
+    assert torch.equal(o, o_kt)
+    # Strided views ([B, N, H, D] memory) give the bitwise same result.
+    qs, ks, vs = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (qd, kd, vd))
+    assert qs.stride() != qd.stride()
+    assert torch.equal(_run(qs, ks, vs), o)
+    # Deterministic across launches.
+    assert torch.equal(_run(qd, kd, vd), o)
+
+
+def test_c2_key_permutation_property():
+    dev = _cuda()
+    from grammar.workloads import C2, attention_inputs
+    q, k, v = (t.to(dev) for t in attention_inputs(C2, seed=5))
+    perm = torch.randperm(C2.N, generator=torch.Generator("cpu").manual_seed(1)).to(dev)
+    a = _run(q, k, v).float()
+    b = _run(q, k[:, :, perm].contiguous(), v[:, :, perm].contiguous()).float()
+    assert (a - b).abs().max().item() <= 2e-3
+
+
+def test_c3_causal_bf16_full_size():
+    dev = _cuda()
+    from grammar.workloads import C3, attention_inputs
+    q, k, v = attention_inputs(C3, seed=0)
+    o = _run(q.to(dev), k.to(dev), v.to(dev), causal=True).float().cpu()
+    assert torch.isfinite(o).all()
+    # O[i] is a convex combination of V[0..i]: inside each head's V hull.
+    vf = v.float()
+    lo = vf.amin(dim=2, keepdim=True) - 1e-2
+    hi = vf.amax(dim=2, keepdim=True) + 1e-2
+    assert bool(((o >= lo) & (o <= hi)).all())
+    # Row 0 attends only to key 0: O[.,.,0] == V[.,.,0] up to bf16 rounding.
+    assert (o[:, :, 0] - vf[:, :, 0]).abs().max().item() <= 1e-2
+    # Oracle on a sample of heads (each is a 4096x4096 fp32 problem on the CPU).
+    for b, h in ((0, 0), (1, 31), (0, 17)):
+        ref = O.attention(q[b, h].float().numpy(), k[b, h].float().numpy(), v[b, h].float().numpy(), causal=True)
+        _check(o[b, h], ref, f"C3 head ({b},{h})")
+
+
+def test_rejects_bad_shapes():
+    dev = _cuda()
+    from grammar import runtime as rt
+    q = torch.zeros(1, 1, 200, 64, dtype=torch.float16, device=dev)
+    with pytest.raises(rt.GrError):
+        _run(q, q, q)                        # N not a multiple of the tile
+    q = torch.zeros(1, 1, 256, 96, dtype=torch.float16, device=dev)
+    with pytest.raises(rt.GrError):
+        _run(q, q, q)                        # unsupported head dim
+    with pytest.raises(ValueError):
+        from grammar.attention import flash_attention_fwd
+        flash_attention_fwd(q.cpu(), q.cpu(), q.cpu())   # no CPU path
