@@ -66,6 +66,21 @@ def cpu_baseline(cfg, seed: int, budget_s: float = 12.0) -> dict:
     }
 
 
+def measured_traffic(cfg, bm: int, bn: int):
+    """HBM bytes per launch for this kernel configuration from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE measurement (profiles/traffic.json),
+    scaled by the copy-calibration factors; None if not measured."""
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        k = t["kernels"][f"{cfg.name}:{cfg.dtype}:bm{bm}:bn{bn}"]
+        c = t["calibration"]
+        return int((k["fetch_kib"] * c["fetch_factor"] + k["write_kib"] * c["write_factor"]) * 1024)
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -74,6 +89,11 @@ def main() -> int:
     ap.add_argument("--config", default="C2", choices=["C2", "C3"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--block-m", type=int, default=128, help="queries per workgroup")
+    ap.add_argument("--block-n", type=int, default=128, help="keys per tile")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="instead of the benchmark, run --steps plain device copies of MIB MiB "
+                         "(the known-size reference that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -85,11 +105,23 @@ def main() -> int:
     from grammar.attention import flash_attention_fwd
     from grammar.workloads import CONFIGS, attention_inputs
 
-    cfg = CONFIGS[args.config]
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(max(1, args.steps)):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: {args.steps} copies of {args.copy_calibration} MiB")
+        return 0
+
+    cfg = CONFIGS[args.config]
+    if cfg.D == 128 and args.block_n > 64:
+        args.block_n = 64
     q, k, v = (t.to(dev) for t in attention_inputs(cfg, seed=args.seed))
     out = torch.empty_like(q)
-    kernel = {"name": "gr_flash_fwd (hand-written)", "block_m": 128, "block_n": 64}
+    kernel = {"name": "gr_flash_fwd (hand-written)", "block_m": args.block_m, "block_n": args.block_n}
 
     def step():
         flash_attention_fwd(q, k, v, causal=cfg.causal, out=out,
@@ -138,7 +170,8 @@ def main() -> int:
         "pct_peak": round(100 * tflops / peak, 2),
         "evals_per_min": None,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(tflops / peak, 5), "traffic": None},
+                     "frac": round(tflops / peak, 5),
+                     "traffic": measured_traffic(cfg, args.block_m, args.block_n)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

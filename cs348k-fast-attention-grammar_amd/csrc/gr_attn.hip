@@ -10,7 +10,7 @@
 
 namespace {
 
-template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT>
+template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT, bool PIPE = false>
 int launch_flash(const gr_attn_args& a, hipStream_t st) {
   constexpr int BM = NW * QB * 32;
   constexpr int LDS = gr_flash_lds<D, BN>::BYTES;
@@ -18,7 +18,7 @@ int launch_flash(const gr_attn_args& a, hipStream_t st) {
     return gr::fail(GR_E_ARG, "gr_attn_fwd: N=%d must be a multiple of block_m=%d and block_n=%d", a.N, BM, BN);
   const long long nblk = (long long)a.B * a.H * (a.N / BM);
   if (nblk <= 0 || nblk > 0x7fffffffLL) return gr::fail(GR_E_ARG, "gr_attn_fwd: grid size %lld out of range", nblk);
-  hipLaunchKernelGGL((gr_flash_fwd_kernel<T, D, BN, NW, QB, CAUSAL, KT>), dim3((unsigned)nblk), dim3(NW * 64), LDS,
+  hipLaunchKernelGGL((gr_flash_fwd_kernel<T, D, BN, NW, QB, CAUSAL, KT, PIPE>), dim3((unsigned)nblk), dim3(NW * 64), LDS,
                      st, a);
   return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_fwd launch");
 }
@@ -31,9 +31,12 @@ int dispatch_tiles(const gr_attn_args& a, int bm, int bn, hipStream_t st) {
   if (bn == 0) bn = 64;
   if (bm == 128 && bn == 64) return launch_flash<T, D, 64, 4, 1, CAUSAL, KT>(a, st);
   if (bm == 128 && bn == 32) return launch_flash<T, D, 32, 4, 1, CAUSAL, KT>(a, st);
-  if (bm == 128 && bn == 128) return launch_flash<T, D, 128, 4, 1, CAUSAL, KT>(a, st);
   if (bm == 64 && bn == 64) return launch_flash<T, D, 64, 2, 1, CAUSAL, KT>(a, st);
+  // block_m = 129 / 257 select the software-pipelined schedule (tuning probe).
+  if (bm == 129 && bn == 64) return launch_flash<T, D, 64, 4, 1, CAUSAL, KT, true>(a, st);
+  if (bm == 129 && bn == 32) return launch_flash<T, D, 32, 4, 1, CAUSAL, KT, true>(a, st);
   if constexpr (D == 64) {
+    if (bm == 128 && bn == 128) return launch_flash<T, D, 128, 4, 1, CAUSAL, KT>(a, st);
     if (bm == 256 && bn == 64) return launch_flash<T, D, 64, 4, 2, CAUSAL, KT>(a, st);
     if (bm == 256 && bn == 32) return launch_flash<T, D, 32, 4, 2, CAUSAL, KT>(a, st);
   }

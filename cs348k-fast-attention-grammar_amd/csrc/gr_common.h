@@ -6,6 +6,9 @@
 // Self-contained on purpose: hiprtc compiles it without the C++ standard
 // library, so nothing here includes a system header beyond what hiprtc provides.
 #pragma once
+#ifndef __HIPCC_RTC__
+#include <hip/hip_runtime.h>
+#endif
 
 #ifndef GR_INF
 #define GR_INF __builtin_inff()
@@ -17,6 +20,7 @@ typedef _Float16 gr_f16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 gr_bf16x4 __attribute__((ext_vector_type(4)));
 typedef float gr_f32x16 __attribute__((ext_vector_type(16)));
 typedef float gr_f32x4 __attribute__((ext_vector_type(4)));
+typedef float gr_f32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int gr_u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int gr_u32x2 __attribute__((ext_vector_type(2)));
 
@@ -31,9 +35,18 @@ typedef unsigned int gr_u32x2 __attribute__((ext_vector_type(2)));
 // ---------------------------------------------------------------------------
 template <class T> struct gr_mfma;
 
+typedef _Float16 gr_f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 gr_bf16x2 __attribute__((ext_vector_type(2)));
+
 template <> struct gr_mfma<_Float16> {
   typedef gr_f16x8 vec8;
   typedef gr_f16x4 vec4;
+  typedef gr_f16x2 vec2;
+  // acc + a.x + a.y, products exact, fp32 accumulate (v_dot2c_f32_f16).
+  static __device__ __forceinline__ float sum2(vec2 a, float acc) {
+    const vec2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(a, one, acc, false);
+  }
   static __device__ __forceinline__ gr_f32x16 mma32(vec8 a, vec8 b, gr_f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
@@ -45,6 +58,11 @@ template <> struct gr_mfma<_Float16> {
 template <> struct gr_mfma<__bf16> {
   typedef gr_bf16x8 vec8;
   typedef gr_bf16x4 vec4;
+  typedef gr_bf16x2 vec2;
+  static __device__ __forceinline__ float sum2(vec2 a, float acc) {
+    const vec2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(a, one, acc, false);
+  }
   static __device__ __forceinline__ gr_f32x16 mma32(vec8 a, vec8 b, gr_f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
@@ -89,3 +107,6 @@ __device__ __forceinline__ int gr_xcd_remap(int bid, int nblk) {
   if ((nblk & 7) != 0) return bid;
   return (bid & 7) * (nblk >> 3) + (bid >> 3);
 }
+
+// Wave-uniform "any lane" vote.
+__device__ __forceinline__ bool gr_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }

@@ -40,6 +40,7 @@ struct gr_attn_args {
   float scale_log2;             // softmax scale * log2(e)
 };
 
+template <int V> struct gr_ic { static constexpr int value = V; };
 template <bool C, class X, class Y> struct gr_cond { typedef X type; };
 template <class X, class Y> struct gr_cond<false, X, Y> { typedef Y type; };
 
@@ -48,49 +49,64 @@ __device__ __forceinline__ int gr_perm32(int r) {
   return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
 }
 
-// XOR swizzle of the 16-byte chunk index inside an LDS row of CPR chunks, so
-// that 8 consecutive rows read at the same logical chunk hit distinct banks.
+// XOR swizzle of the 16-byte chunk index inside an LDS row of CPR chunks.
+// A 16-byte LDS access by a wavefront is served 8 lanes (32 banks) or 16 lanes
+// (64 banks) at a time; the MFMA operand reads put consecutive rows of an
+// aligned 16-row group on consecutive lanes, all at the same logical chunk.
+// Each mapping below gives those rows distinct bank groups under both bank
+// counts, and is a bit-linear (XOR) function of the row.
 template <int CPR>
 __device__ __forceinline__ int gr_swz(int row, int chunk) {
-  if constexpr (CPR >= 8) return chunk ^ (row & 7);
-  else if constexpr (CPR == 4) return chunk ^ ((row >> 1) & 3);
-  else if constexpr (CPR == 2) return chunk ^ ((row >> 2) & 1);
+  if constexpr (CPR >= 16) return chunk ^ (row & 15);                         // 256+ B rows
+  else if constexpr (CPR == 8) return chunk ^ ((row ^ (row >> 3)) & 7);       // 128 B rows
+  else if constexpr (CPR == 4) return chunk ^ (((row >> 1) ^ (row >> 3)) & 3);  // 64 B rows
+  else if constexpr (CPR == 2) return chunk ^ (((row >> 2) ^ (row >> 3)) & 1);  // 32 B rows
   else return chunk;
 }
 
 // Global [ROWS][COLS] tile (row stride ld elements) -> LDS rows, same shape.
+// Per-thread global and LDS offsets are computed once (init) and reused for
+// every tile, so the main loop spends no VALU on address arithmetic.
 template <class T, int ROWS, int COLS, int NT, bool PERM>
 struct gr_row_loader {
   static constexpr int CPR = COLS / 8;
   static constexpr int CHUNKS = ROWS * CPR;
   static constexpr int PER = (CHUNKS + NT - 1) / NT;
   gr_u32x4 r[PER];
-  __device__ __forceinline__ void gload(const T* src, long long ld, int tid) {
+  int goff[PER];
+  int loff[PER];
+  __device__ __forceinline__ void init(int tid, long long ld) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int c = tid + i * NT;
-      if (CHUNKS % NT == 0 || c < CHUNKS) {
-        const int row = c / CPR, cc = c % CPR;
-        r[i] = gr_ld16(src + (long long)row * ld + cc * 8);
-      }
+      const int row = c / CPR, cc = c % CPR;
+      const int prow = PERM ? gr_perm32(row) : row;
+      goff[i] = (int)(row * ld) + cc * 8;
+      loff[i] = prow * (COLS * 2) + gr_swz<CPR>(prow, cc) * 16;
     }
+  }
+  __device__ __forceinline__ bool live(int i, int tid) const { return CHUNKS % NT == 0 || tid + i * NT < CHUNKS; }
+  __device__ __forceinline__ void gload(const T* src, int tid) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (live(i, tid)) r[i] = gr_ld16(src + goff[i]);
   }
   __device__ __forceinline__ void sstore(char* dst, int tid) const {
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int c = tid + i * NT;
-      if (CHUNKS % NT == 0 || c < CHUNKS) {
-        const int row = c / CPR, cc = c % CPR;
-        const int prow = PERM ? gr_perm32(row) : row;
-        gr_st16(dst + prow * (COLS * 2) + gr_swz<CPR>(prow, cc) * 16, r[i]);
-      }
-    }
+    for (int i = 0; i < PER; ++i)
+      if (live(i, tid)) gr_st16(dst + loff[i], r[i]);
   }
 };
 
 // Global [SR][SC] tile (row stride ld) -> LDS [SC][SR] (transposed). Each unit
 // takes two source rows x 8 columns and writes 8 dwords, each holding the pair
 // of source-row values for one destination row.
+//
+// LDS address of (destination row, source-row pair p): row * SR*2 | chunk*16 |
+// (p & 3)*4 with chunk = (p >> 2) ^ h(row) -- three bit-disjoint fields that are
+// linear over GF(2) in the bits of (unit, e). Hence addr(unit, e) =
+// addr(unit, 0) ^ addr(0, e): one base register per unit and a compile-time
+// constant per destination row e.
 template <class T, int SR, int SC, int NT, bool PERM>
 struct gr_tr_loader {
   static constexpr int PAIRS = SR / 2;
@@ -98,36 +114,46 @@ struct gr_tr_loader {
   static constexpr int UNITS = PAIRS * SCPR;
   static constexpr int PER = (UNITS + NT - 1) / NT;
   static constexpr int DCPR = SR / 8;
+  static_assert((SR & (SR - 1)) == 0 && SR >= 16, "SR must be a power of two");
   gr_u32x4 r0[PER], r1[PER];
-  __device__ __forceinline__ void gload(const T* src, long long ld, int tid) {
+  int goff[PER];
+  int ld1;
+  int lbase[PER];
+  static __device__ __forceinline__ int addr(int drow, int p) {
+    const int prow = PERM ? gr_perm32(drow) : drow;
+    return prow * (SR * 2) + gr_swz<DCPR>(prow, p >> 2) * 16 + (p & 3) * 4;
+  }
+  __device__ __forceinline__ void init(int tid, long long ld) {
+    ld1 = (int)ld;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int u = tid + i * NT;
-      if (UNITS % NT == 0 || u < UNITS) {
-        const int p = u % PAIRS, cc = u / PAIRS;
-        r0[i] = gr_ld16(src + (long long)(2 * p) * ld + cc * 8);
-        r1[i] = gr_ld16(src + (long long)(2 * p + 1) * ld + cc * 8);
-      }
+      const int p = u % PAIRS, cc = u / PAIRS;
+      goff[i] = (int)(2 * p * ld) + cc * 8;
+      lbase[i] = addr(cc * 8, p);
     }
+  }
+  __device__ __forceinline__ bool live(int i, int tid) const { return UNITS % NT == 0 || tid + i * NT < UNITS; }
+  __device__ __forceinline__ void gload(const T* src, int tid) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (live(i, tid)) {
+        r0[i] = gr_ld16(src + goff[i]);
+        r1[i] = gr_ld16(src + goff[i] + ld1);
+      }
   }
   __device__ __forceinline__ void sstore(char* dst, int tid) const {
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int u = tid + i * NT;
-      if (UNITS % NT == 0 || u < UNITS) {
-        const int p = u % PAIRS, cc = u / PAIRS;
+    for (int i = 0; i < PER; ++i)
+      if (live(i, tid)) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const unsigned int w0 = r0[i][e >> 1], w1 = r1[i][e >> 1];
-          const unsigned int w = (e & 1) ? ((w0 >> 16) | (w1 & 0xffff0000u))
-                                         : ((w0 & 0xffffu) | (w1 << 16));
-          const int drow = cc * 8 + e;
-          const int prow = PERM ? gr_perm32(drow) : drow;
-          *reinterpret_cast<unsigned int*>(dst + prow * (SR * 2) +
-                                           gr_swz<DCPR>(prow, p >> 2) * 16 + (p & 3) * 4) = w;
+          const unsigned int w = (e & 1) ? __builtin_amdgcn_perm(w1, w0, 0x07060302u)
+                                         : __builtin_amdgcn_perm(w1, w0, 0x05040100u);
+          *reinterpret_cast<unsigned int*>(dst + (lbase[i] ^ addr(e, 0))) = w;
         }
       }
-    }
   }
 };
 
@@ -138,10 +164,33 @@ struct gr_flash_lds {
   static constexpr int BYTES = 2 * (KS + VT);
 };
 
-template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT>
+// One key tile of S^T = K Q^T for this wave: s[kb][qb] (32 keys x 32 queries
+// per block). K rows sit in LDS with the row permutation gr_perm32.
+template <class T, int D, int BN, int QB>
+__device__ __forceinline__ void gr_flash_qk(gr_f32x16 (&s)[BN / 32][QB], const char* ks,
+                                            const typename gr_mfma<T>::vec8 (&qf)[QB][D / 16], int l32, int g) {
+  typedef typename gr_mfma<T>::vec8 vec8;
+#pragma unroll
+  for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) s[kb][qb] = (gr_f32x16)(0.f);
+#pragma unroll
+  for (int kb = 0; kb < BN / 32; ++kb) {
+    const int row = kb * 32 + l32;
+#pragma unroll
+    for (int ds = 0; ds < D / 16; ++ds) {
+      const vec8 af = gr_as<vec8>(gr_ld16(ks + row * (D * 2) + gr_swz<D / 8>(row, 2 * ds + g) * 16));
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) s[kb][qb] = gr_mfma<T>::mma32(af, qf[qb][ds], s[kb][qb]);
+    }
+  }
+}
+
+template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT, bool PIPE>
 __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* lds) {
   typedef gr_mfma<T> MF;
   typedef typename MF::vec8 vec8;
+  typedef typename MF::vec2 vec2;
   constexpr int BM = NW * QB * 32;
   constexpr int NT = NW * 64;
   constexpr int KB = BN / 32;      // 32-key blocks per tile
@@ -194,45 +243,49 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
   typedef gr_tr_loader<T, BN, D, NT, false> VLoad;
   typename gr_cond<KT_LAYOUT, KCols, KRows>::type kl;
   VLoad vl;
+  kl.init(tid, a.k_sn);
+  vl.init(tid, a.v_sn);
+  // Element offset of key tile t in K (KT layout: a column offset).
+  const long long k_tile = KT_LAYOUT ? (long long)BN : (long long)BN * a.k_sn;
+  const long long v_tile = (long long)BN * a.v_sn;
 
   const int ntile = CAUSAL ? (q0 + BM + BN - 1) / BN : a.N / BN;
+  const int wq_last = qw + QB * 32 - 1;        // this wave's last query
+  auto wave_active = [&](int t) { return !CAUSAL || t * BN <= wq_last; };
 
-  auto gload = [&](int t) {
-    if constexpr (KT_LAYOUT) kl.gload(Kp + t * BN, a.k_sn, tid);
-    else kl.gload(Kp + (long long)t * BN * a.k_sn, a.k_sn, tid);
-    vl.gload(Vp + (long long)t * BN * a.v_sn, a.v_sn, tid);
-  };
-  auto sstore = [&](int buf) {
-    kl.sstore(ks0 + buf * L::KS, tid);
-    vl.sstore(vt0 + buf * L::VT, tid);
-  };
+  // LDS ring: K_j and V_j live in slot j & 1. With PIPE the scores of tile
+  // t+1 are computed during iteration t (on the matrix cores, while tile t's
+  // softmax runs on the vector ALUs): iteration t reads K_{t+1} and V_t and then
+  // stores K_{t+2}, V_{t+1} into the slots K_t and V_{t-1} occupied. Without
+  // PIPE iteration t reads K_t, V_t and stores K_{t+1}, V_{t+1}.
+  constexpr int KAHEAD = PIPE ? 2 : 1;
+  kl.gload(Kp, tid);
+  vl.gload(Vp, tid);
+  kl.sstore(ks0, tid);
+  vl.sstore(vt0, tid);
+  if (PIPE && ntile > 1) {
+    kl.gload(Kp + k_tile, tid);
+    kl.sstore(ks0 + L::KS, tid);
+  }
+  __syncthreads();
+  // Two score buffers used in turn (the loop is unrolled by two), so handing
+  // the next tile's scores over costs no register moves.
+  gr_f32x16 sA[KB][QB], sB[PIPE ? KB : 1][QB];
+  if (PIPE) {
+    gr_flash_qk<T, D, BN, QB>(sA, ks0, qf, l32, g);
+    __syncthreads();   // every wave is done with slot 0 of K before K_2 lands there
+  }
 
-  gload(0);
-  sstore(0);
-  for (int t = 0; t < ntile; ++t) {
-    const int cur = t & 1;
-    if (t + 1 < ntile) gload(t + 1);
-    __syncthreads();
+  // One key tile. s: this tile's scores; sn: next tile's (PIPE only).
+  // Slots are compile-time in each unrolled copy (ODD = t & 1).
+  auto tile = [&](const int t, auto odd_tag, auto& s, auto& sn) {
+    constexpr int ODD = decltype(odd_tag)::value;
+    const bool pf_k = t + KAHEAD < ntile, pf_v = t + 1 < ntile;
+    if (pf_k) kl.gload(Kp + (t + KAHEAD) * k_tile, tid);
+    if (pf_v) vl.gload(Vp + (t + 1) * v_tile, tid);
     const int k0 = t * BN;
-    const bool active = !CAUSAL || (k0 <= qw + QB * 32 - 1);
-    if (active) {
-      const char* ks = ks0 + cur * L::KS;
-      const char* vt = vt0 + cur * L::VT;
-      gr_f32x16 s[KB][QB];
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) s[kb][qb] = (gr_f32x16)(0.f);
-#pragma unroll
-      for (int ds = 0; ds < DS; ++ds) {
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-          const int row = kb * 32 + l32;
-          const vec8 af = gr_as<vec8>(gr_ld16(ks + row * (D * 2) + gr_swz<D / 8>(row, 2 * ds + g) * 16));
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb) s[kb][qb] = MF::mma32(af, qf[qb][ds], s[kb][qb]);
-        }
-      }
+    if (wave_active(t)) {
+      if constexpr (!PIPE) gr_flash_qk<T, D, BN, QB>(s, ks0 + ODD * L::KS, qf, l32, g);
       if (CAUSAL && k0 + BN - 1 > qw) {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
@@ -246,6 +299,9 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
             }
           }
       }
+      // Running max; the accumulators are rescaled only when some lane's max
+      // grew (otherwise the factor is exactly 1 and the multiply is skipped).
+      float nmc[QB];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
         float mt = -GR_INF;
@@ -255,32 +311,37 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
           for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][qb][r]);
         mt = fmaxf(mt, gr_xor32(mt));
         const float mn = fmaxf(m[qb], mt);
-        const float ms = (mn == -GR_INF) ? 0.f : mn;
-        const float alpha = gr_exp2((m[qb] - ms) * c);
-        const float nmc = -ms * c;
-        float ls = 0.f;
+        if (gr_any(mn > m[qb])) {
+          const float alpha = gr_exp2((m[qb] - mn) * c);   // m = -inf -> 0
+          l[qb] *= alpha;
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float p = gr_exp2(fmaf(s[kb][qb][r], c, nmc));
-            s[kb][qb][r] = p;
-            ls += p;
-          }
-        l[qb] = l[qb] * alpha + ls;
+          for (int db = 0; db < DB; ++db) o[db][qb] *= alpha;
+        }
         m[qb] = mn;
-#pragma unroll
-        for (int db = 0; db < DB; ++db) o[db][qb] *= alpha;
+        nmc[qb] = -((mn == -GR_INF) ? 0.f : mn) * c;
       }
+      if constexpr (PIPE) {
+        if (t + 1 < ntile && wave_active(t + 1)) gr_flash_qk<T, D, BN, QB>(sn, ks0 + (ODD ^ 1) * L::KS, qf, l32, g);
+      }
+      const char* vt = vt0 + ODD * L::VT;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
           vec8 pf[QB];
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb)
+          for (int qb = 0; qb < QB; ++qb) {
+            gr_u32x4 pw;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) pf[qb][e] = (T)s[kb][qb][8 * hf + e];
+            for (int e = 0; e < 8; e += 2) {
+              const float p0 = gr_exp2(fmaf(s[kb][qb][8 * hf + e], c, nmc[qb]));
+              const float p1 = gr_exp2(fmaf(s[kb][qb][8 * hf + e + 1], c, nmc[qb]));
+              const vec2 pp = __builtin_convertvector((gr_f32x2){p0, p1}, vec2);
+              l[qb] = MF::sum2(pp, l[qb]);
+              pw[e >> 1] = __builtin_bit_cast(unsigned int, pp);
+            }
+            pf[qb] = gr_as<vec8>(pw);
+          }
 #pragma unroll
           for (int db = 0; db < DB; ++db) {
             const int row = db * 32 + l32;
@@ -290,7 +351,19 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
           }
         }
     }
-    if (t + 1 < ntile) sstore(cur ^ 1);
+    if (pf_k) kl.sstore(ks0 + (PIPE ? ODD : (ODD ^ 1)) * L::KS, tid);
+    if (pf_v) vl.sstore(vt0 + (ODD ^ 1) * L::VT, tid);
+    __syncthreads();
+  };
+
+  for (int t = 0; t < ntile; t += 2) {
+    if constexpr (PIPE) {
+      tile(t, gr_ic<0>{}, sA, sB);
+      if (t + 1 < ntile) tile(t + 1, gr_ic<1>{}, sB, sA);
+    } else {
+      tile(t, gr_ic<0>{}, sA, sB);
+      if (t + 1 < ntile) tile(t + 1, gr_ic<1>{}, sA, sB);
+    }
   }
 
 #pragma unroll
@@ -310,10 +383,28 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
   }
 }
 
+// Waves per SIMD the kernel is compiled for. Two caps it at 256 VGPRs, which
+// lets the backend keep every MFMA operand and accumulator in VGPRs (no AGPR
+// round trips around the softmax arithmetic); configurations whose estimated
+// live state exceeds that ask for one wave (and use AGPRs) instead of spilling.
+// Estimate (VGPRs/lane): two score buffers QB*BN, output QB*D/2, Q fragments
+// QB*D/4, prefetch registers + offsets of the K and V tile loaders, ~40 misc.
+template <int D, int BN, int NW, int QB, bool KT, bool PIPE>
+struct gr_flash_wpe {
+  static constexpr int NT = NW * 64;
+  static constexpr int K_UNITS = KT ? (D / 2) * (BN / 8) : BN * D / 8;
+  static constexpr int K_REGS = (KT ? 10 : 6) * ((K_UNITS + NT - 1) / NT);
+  static constexpr int V_REGS = 10 * (((BN / 2) * (D / 8) + NT - 1) / NT);
+  static constexpr int EST = (PIPE ? 2 : 1) * QB * BN / 2 + QB * D / 2 + QB * D / 4 + K_REGS + V_REGS + 40;
+  static constexpr int value = EST > 224 ? 1 : 2;
+};
+
 // Kernel wrapper used by the prebuilt library; the grammar renderer emits its
 // own wrappers with baked-in shapes around the same body.
-template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT>
-__global__ __launch_bounds__(NW * 64) void gr_flash_fwd_kernel(gr_attn_args a) {
+template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT, bool PIPE>
+__global__ __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu(gr_flash_wpe<D, BN, NW, QB, KT_LAYOUT, PIPE>::value)))
+void gr_flash_fwd_kernel(gr_attn_args a) {
   extern __shared__ __attribute__((aligned(16))) char gr_lds[];
-  gr_flash_fwd_body<T, D, BN, NW, QB, CAUSAL, KT_LAYOUT>(a, gr_lds);
+  gr_flash_fwd_body<T, D, BN, NW, QB, CAUSAL, KT_LAYOUT, PIPE>(a, gr_lds);
 }

@@ -59,6 +59,7 @@ SMALL = [
     (2, 3, 256, 128, "bf16", True, False, 128, 64),
     (1, 2, 512, 64, "fp16", False, False, 128, 32),
     (1, 2, 512, 64, "fp16", True, False, 128, 128),
+    (1, 2, 512, 64, "bf16", False, False, 128, 128),
     (1, 2, 512, 64, "fp16", False, False, 64, 64),
     (1, 2, 512, 64, "fp16", True, False, 256, 64),
     (1, 2, 512, 64, "bf16", False, True, 256, 32),
