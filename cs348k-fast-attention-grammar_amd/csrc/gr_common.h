@@ -14,6 +14,10 @@
 #define GR_INF __builtin_inff()
 #endif
 
+// Marks, in generated code, the per-iteration offset of a sub-tile read from a
+// value materialised outside a ReductionLoop (an extract bridge).
+#define GR_SUBTILE(x) (x)
+
 typedef _Float16 gr_f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 gr_bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 gr_f16x4 __attribute__((ext_vector_type(4)));

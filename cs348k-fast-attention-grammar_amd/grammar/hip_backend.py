@@ -1,0 +1,769 @@
+"""HIP (gfx950) renderer for grammar programs.
+
+render_module(program) -> one HIP C++ translation unit: an extern "C" kernel
+per ParallelLoop stage, plus a trailing /*GR_PLAN ...*/ comment holding the
+launch plan (kernel, grid, block, LDS bytes, tensor arguments) and
+KERNEL_META. The source alone is a durable, re-runnable artefact (the
+reference keeps emitted cuTile modules the same way, grammar/optimization.py:
+869-876).
+
+Lowering, per stage (first match wins):
+  * flash: one ReductionLoop over the key axis whose single partial is
+    softmax_matmul(x, V) with x = [causal](mulc(matmul(Q, KT), scale)) computed
+    inside the loop -> the hand-written CDNA4 body in gr_flash_fwd.h,
+    instantiated with the stage's query tile, the loop's key tile, the
+    program's scale/mask and storage type (fp16/bf16).
+  * generic: every other stage. Each tile lives in LDS as fp32 (row-major in
+    its materialised shape); statements run in program order across the 256
+    threads of the workgroup with a barrier after each; values produced
+    outside a ReductionLoop are read as per-iteration sub-tile views (the
+    reference's ct.extract); ReductionLoop partials accumulate in fp32
+    (matmul: sum of products, rowmax/rowsum, online softmax). Loads convert
+    from and stores convert to the storage type.
+Unsupported structures raise UnsupportedProgram (the Evaluator scores them as
+infeasible), never a silent fallback.
+"""
+from __future__ import annotations
+
+import json
+import math
+import re
+
+from .kernel_ast import (
+    Program, ParallelLoop, Load, Store, Compute, ReductionLoop, ROW_REDUCE_OPS, ELEMENTWISE_OPS,
+    _infer_program, _resolve_index, _value_axes, _program_io, _loop_tensors, validate, kernel_meta,
+    _loads_feeding, _iter_loads, _axis_global_extent,
+)
+
+NT = 256                      # threads per workgroup of generic kernels
+LDS_LIMIT = 160 * 1024        # gfx950 LDS per workgroup
+CTYPE = {"fp32": "float", "fp16": "_Float16", "bf16": "__bf16"}
+LOG2E = 1.4426950408889634
+
+
+class UnsupportedProgram(Exception):
+    """The program uses a structure this renderer cannot lower."""
+
+
+class LdsOverflow(UnsupportedProgram):
+    """A stage needs more LDS than one gfx950 workgroup has."""
+
+    def __init__(self, stage, need):
+        super().__init__(f"stage {stage}: needs {need} bytes of LDS > {LDS_LIMIT}")
+        self.need = need
+
+
+def _cname(name: str) -> str:
+    """C identifier for a tensor: prefixed so no tensor name can collide with
+    the generated code's locals (e, k, i0, ...)."""
+    return "t_" + re.sub(r"[^A-Za-z0-9_]", "_", name)
+
+
+def _prod(xs):
+    return math.prod(xs) if xs else 1
+
+
+def _cdiv(a, b):
+    return -(-a // b)
+
+
+def _flt(x: float) -> str:
+    r = repr(float(x))
+    if "inf" in r or "nan" in r:
+        raise UnsupportedProgram(f"non-finite constant {x}")
+    return r + "f"
+
+
+# ---------------------------------------------------------------------------
+# Flash lowering
+# ---------------------------------------------------------------------------
+FLASH_BM = {32: (1, 1), 64: (2, 1), 128: (4, 1), 256: (4, 2)}   # block_m -> (waves, query blocks/wave)
+
+
+def _match_flash(loop: ParallelLoop, program: Program):
+    """Return the flash parameters if `loop` is the flash pattern, else None."""
+    if program.dtype not in ("fp16", "bf16"):
+        return None
+    reds = [s for s in loop.body if isinstance(s, ReductionLoop)]
+    stores = [s for s in loop.body if isinstance(s, Store)]
+    if len(reds) != 1 or len(stores) != 1 or len(reds[0].partials) != 1:
+        return None
+    rl, st = reds[0], stores[0]
+    smm = rl.partial
+    if not (isinstance(smm, Compute) and smm.op == "softmax_matmul" and smm.axis == rl.axis):
+        return None
+    if st.src is not rl or st.dest != loop.out:
+        return None
+    x, vload = smm.inputs
+    if not isinstance(vload, Load):
+        return None
+    inner = {id(s) for s in rl.body}
+    causal, scale = False, 1.0
+    if isinstance(x, Compute) and x.op == "causal":
+        if x.axis != rl.axis or id(x) not in inner:
+            return None
+        causal, x = True, x.inputs[0]
+    if isinstance(x, Compute) and x.op == "mulc":
+        if id(x) not in inner:
+            return None
+        scale, x = float(x.const), x.inputs[0]
+    if isinstance(x, Compute) and x.op == "causal" and not causal:
+        if x.axis != rl.axis or id(x) not in inner:
+            return None
+        causal, x = True, x.inputs[0]
+    if not (isinstance(x, Compute) and x.op == "matmul" and id(x) in inner):
+        return None
+    qload, ktload = x.inputs
+    if not (isinstance(qload, Load) and isinstance(ktload, Load)):
+        return None
+    # other statements must be exactly these loads/computes
+    allowed = {id(rl), id(st), id(qload), id(ktload), id(vload), id(smm), id(x)}
+    chain = smm.inputs[0]
+    while isinstance(chain, Compute) and chain is not x:
+        allowed.add(id(chain))
+        chain = chain.inputs[0]
+    for s in list(loop.body) + list(rl.body):
+        if id(s) not in allowed:
+            return None
+    T = program.tensors
+    qs, kts, vs, os_ = T[qload.source], T[ktload.source], T[vload.source], T[loop.out]
+    nb = len(qs) - 2
+    if nb < 0 or len(kts) != len(qs) or len(vs) != len(qs) or len(os_) != len(qs):
+        return None
+    iv = list(loop.index_vars)
+    if len(iv) != len(qs):
+        return None
+    bax, iax, dax = iv[:nb], iv[nb], iv[nb + 1]
+    jax = rl.axis
+    if qload.index != bax + [iax, dax] or ktload.index != bax + [dax, jax] or \
+            vload.index != bax + [jax, dax] or st.index != bax + [iax, dax]:
+        return None
+    N, D = qs[-2], qs[-1]
+    if tuple(kts[-2:]) != (D, N) or tuple(vs[-2:]) != (N, D) or tuple(os_) != tuple(qs) or \
+            tuple(kts[:nb]) != tuple(qs[:nb]) or tuple(vs[:nb]) != tuple(qs[:nb]):
+        return None
+    tile = loop.tile_shape
+    if any(t != 1 for t in tile[:nb]):
+        return None
+    BM, BN = tile[nb], rl.tile
+    if tile[nb + 1] < D:
+        return None
+    if BM not in FLASH_BM or BN not in (32, 64, 128) or D not in (64, 128):
+        return None
+    if D == 128 and BN > 64:
+        return None
+    if N % BM or N % BN:
+        return None
+    nw, qb = FLASH_BM[BM]
+    if D == 128 and qb > 1:
+        return None
+    return {"q": qload.source, "kt": ktload.source, "v": vload.source, "o": loop.out,
+            "lead": _prod(qs[:nb]), "N": N, "D": D, "BM": BM, "BN": BN, "NW": nw, "QB": qb,
+            "causal": causal, "scale": scale}
+
+
+def _render_flash(loop, program, f) -> tuple:
+    T = CTYPE[program.dtype]
+    kname = f"{_cname(loop.out)}_kernel"
+    args = _loop_tensors(loop)
+    params = ", ".join(f"{'const ' if a != loop.out else ''}{T}* __restrict__ {_cname(a)}" for a in args)
+    N, D = f["N"], f["D"]
+    pipe = "false"
+    nt = f["NW"] * 64
+    code = f"""
+// stage {loop.out}: flash attention (online softmax over key tiles of {f['BN']}, {f['BM']} queries/workgroup)
+extern "C" __global__ __launch_bounds__({nt})
+__attribute__((amdgpu_waves_per_eu(gr_flash_wpe<{D}, {f['BN']}, {f['NW']}, {f['QB']}, true, {pipe}>::value)))
+void {kname}({params}) {{
+  extern __shared__ __attribute__((aligned(16))) char gr_flash_smem[];
+  gr_attn_args a;
+  a.q = {_cname(f['q'])}; a.k = {_cname(f['kt'])}; a.v = {_cname(f['v'])}; a.o = {_cname(f['o'])};
+  a.q_sb = {N * D}LL; a.q_sh = 0; a.q_sn = {D};
+  a.k_sb = {N * D}LL; a.k_sh = 0; a.k_sn = {N};
+  a.v_sb = {N * D}LL; a.v_sh = 0; a.v_sn = {D};
+  a.o_sb = {N * D}LL; a.o_sh = 0; a.o_sn = {D};
+  a.B = {f['lead']}; a.H = 1; a.N = {N};
+  a.scale_log2 = {_flt(f['scale'] * LOG2E)};
+  gr_flash_fwd_body<{T}, {D}, {f['BN']}, {f['NW']}, {f['QB']}, {'true' if f['causal'] else 'false'}, true, {pipe}>(a, gr_flash_smem);
+}}
+"""
+    grid = f["lead"] * (N // f["BM"])
+    lds = 2 * (f["BN"] * D * 2 + D * f["BN"] * 2)
+    return code, {"kernel": kname, "grid": [grid, 1, 1], "block": [nt, 1, 1], "lds": lds,
+                  "args": args, "lowering": "flash",
+                  "tiles": {"block_m": f["BM"], "block_n": f["BN"]}}
+
+
+# ---------------------------------------------------------------------------
+# Generic lowering
+# ---------------------------------------------------------------------------
+class _View:
+    """A tile as seen from the current scope: LDS base (floats), shape, the
+    strides of the buffer it lives in, a dynamic offset expression, axes."""
+
+    def __init__(self, base, shape, strides, dyn, axes, origin):
+        self.base, self.shape, self.strides, self.dyn, self.axes = base, tuple(shape), tuple(strides), dyn, list(axes)
+        self.origin = list(origin)     # C expression: global index of element 0, per axis
+
+    def addr(self, idx_exprs) -> str:
+        parts = [str(self.base)]
+        if self.dyn:
+            parts.append(f"({self.dyn})")
+        for d, (e, s) in enumerate(zip(idx_exprs, self.strides)):
+            if self.shape[d] > 1 and s:
+                parts.append(f"({e})*{s}" if s != 1 else f"({e})")
+        return " + ".join(parts)
+
+
+def _row_major(shape):
+    st, acc = [], 1
+    for n in reversed(shape):
+        st.append(acc)
+        acc *= n
+    return tuple(reversed(st))
+
+
+class _StageGen:
+    def __init__(self, loop: ParallelLoop, program: Program, shapes: dict):
+        self.loop, self.p, self.shapes = loop, program, shapes
+        self.T = CTYPE[program.dtype]
+        self.lines = []
+        self.ind = 1
+        self.bufs = {}                 # LDS buffer name -> {size (floats), def, last}
+        self.pos = 0                   # statement position (buffer lifetimes)
+        self.nfl = 0                   # LDS floats after allocation
+        self.vals = {}                 # id -> (base, shape, axes, depth, origin)
+        self.loops = []                # enclosing ReductionLoops
+        self.scope = {}                # index name -> C expression of its tile coordinate
+        self.n = 0
+
+    # -- helpers -----------------------------------------------------------
+    def emit(self, s):
+        self.lines.append("  " * self.ind + s)
+
+    def fresh(self, p="v"):
+        self.n += 1
+        return f"{p}{self.n}"
+
+    def alloc(self, shape) -> str:
+        """A symbolic LDS buffer; offsets are assigned from lifetimes at the end."""
+        name = f"B{len(self.bufs)}"
+        self.bufs[name] = {"size": (max(1, _prod(shape)) + 3) & ~3, "def": self.pos, "last": self.pos}
+        return name
+
+    def touch(self, name):
+        b = self.bufs[name]
+        b["last"] = max(b["last"], self.pos)
+
+    def step(self):
+        self.pos += 1
+
+    def assign_lds(self) -> list:
+        """First-fit placement of buffers whose [def, last] intervals overlap."""
+        placed, offs = [], {}
+        for name in sorted(self.bufs, key=lambda n: (self.bufs[n]["def"], n)):
+            b = self.bufs[name]
+            conf = sorted((o, sz) for (o, sz, d, l) in placed if not (l < b["def"] or d > b["last"]))
+            off = 0
+            for o, sz in conf:
+                if off + b["size"] <= o:
+                    break
+                off = max(off, o + sz)
+            placed.append((off, b["size"], b["def"], b["last"]))
+            offs[name] = off
+        self.nfl = max((o + sz for o, sz, _, _ in placed), default=0)
+        return [f"  constexpr int {n} = {offs[n]};" for n in sorted(offs, key=lambda x: int(x[1:]))]
+
+    def sync(self):
+        self.emit("__syncthreads();")
+
+    def define(self, node, base, shape, axes, origin):
+        if len(origin) != len(axes):
+            raise UnsupportedProgram("internal: origin/axes rank mismatch")
+        self.vals[id(node)] = (base, tuple(shape), list(axes), len(self.loops), list(origin))
+
+    def view(self, node) -> _View:
+        if id(node) not in self.vals:
+            raise UnsupportedProgram(f"value {type(node).__name__} used before it is produced")
+        base, shape, axes, d0, origin = self.vals[id(node)]
+        self.touch(base)
+        strides = _row_major(shape)
+        shape, origin = list(shape), list(origin)
+        dyn = []
+        for lp in self.loops[d0:]:
+            if lp.axis in axes:
+                p = axes.index(lp.axis)
+                if shape[p] > lp.tile:
+                    if shape[p] % lp.tile:
+                        raise UnsupportedProgram("sub-tile does not divide the materialised tile")
+                    dyn.append(f"GR_SUBTILE({self.loopvar(lp)}*{lp.tile * strides[p]})")
+                    shape[p] = lp.tile
+                    origin[p] = f"({origin[p]}) + {self.loopvar(lp)}*{lp.tile}"
+        return _View(base, shape, strides, " + ".join(dyn), axes, origin)
+
+    def loopvar(self, lp):
+        return f"kk_{_cname(lp.axis)}_{id(lp) % 100000}"
+
+    def elem_loop(self, shape, body_fn):
+        """for (e in tile) with per-dim index names i0..; body_fn(idx_exprs, e)."""
+        E = _prod(shape)
+        self.emit(f"for (int e = threadIdx.x; e < {E}; e += {NT}) {{")
+        self.ind += 1
+        idx = []
+        rem = "e"
+        st = _row_major(shape)
+        for d, n in enumerate(shape):
+            if n == 1:
+                idx.append("0")
+                continue
+            v = f"i{d}"
+            if st[d] == 1:
+                self.emit(f"const int {v} = {rem} % {n};" if d > 0 else f"const int {v} = {rem};")
+            else:
+                self.emit(f"const int {v} = ({rem} / {st[d]}){f' % {n}' if d > 0 else ''};")
+            idx.append(v)
+        body_fn(idx)
+        self.ind -= 1
+        self.emit("}")
+
+    # -- statements ----------------------------------------------------------
+    def gen_body(self, stmts, partial_acc=None):
+        for s in stmts:
+            self.step()
+            if isinstance(s, Load):
+                self.gen_load(s)
+            elif isinstance(s, Compute):
+                if partial_acc is not None and id(s) in partial_acc:
+                    self.gen_partial(s, partial_acc[id(s)])
+                else:
+                    self.gen_compute(s)
+            elif isinstance(s, ReductionLoop):
+                self.gen_reduction(s)
+            elif isinstance(s, Store):
+                self.gen_store(s)
+            else:
+                raise UnsupportedProgram(f"statement {type(s).__name__}")
+
+    def _coords(self, index, tile, g, what):
+        names = _resolve_index(index, tile, g, set(self.scope), what)
+        return [("0" if n == "0" else self.scope[n]) for n in names]
+
+    def gen_load(self, s: Load):
+        shp = self.shapes[id(s)]
+        g = self.p.tensors[s.source]
+        for t, gd in zip(shp, g):
+            if (t < gd and gd % t) or (t > gd and gd != 1):
+                raise UnsupportedProgram(f"load {s.source}: tile {t} does not tile extent {gd}")
+        coords = self._coords(s.index, shp, g, f"load {s.source}")
+        base = self.alloc(shp)
+        gst = _row_major(g)
+        src = _cname(s.source)
+
+        def body(idx):
+            terms = []
+            for d, (c, t) in enumerate(zip(coords, shp)):
+                if g[d] == 1:
+                    continue
+                ix = idx[d] if shp[d] > 1 else "0"
+                e = f"({c})*{t} + {ix}" if c != "0" else ix
+                terms.append(f"(long long)({e})*{gst[d]}" if gst[d] != 1 else f"(long long)({e})")
+            gi = " + ".join(terms) if terms else "0"
+            self.emit(f"gr_lds[{base} + e] = (float){src}[{gi}];")
+        self.elem_loop(shp, body)
+        self.sync()
+        origin = [("0" if (c == "0" or g[d] == 1) else f"({c})*{shp[d]}") for d, c in enumerate(coords)]
+        self.define(s, base, shp, s.index, origin)
+
+    def gen_store(self, s: Store):
+        v = self.view(s.src)
+        g = self.p.tensors[s.dest]
+        tile = self.shapes[id(s.src)]
+        coords = self._coords(s.index, tile, g, f"store {s.dest}")
+        gst = _row_major(g)
+        dst = _cname(s.dest)
+        if len(v.shape) != len(g):
+            raise UnsupportedProgram("store rank mismatch")
+
+        def body(idx):
+            terms, conds = [], []
+            for d, c in enumerate(coords):
+                if g[d] == 1:
+                    continue
+                ix = idx[d] if v.shape[d] > 1 else "0"
+                e = f"({c})*{tile[d]} + {ix}" if c != "0" else ix
+                terms.append(f"(long long)({e})*{gst[d]}" if gst[d] != 1 else f"(long long)({e})")
+                if (c != "0" and tile[d] * _cdiv(g[d], tile[d]) != g[d]) or (c == "0" and v.shape[d] > g[d]):
+                    conds.append(f"({e}) < {g[d]}")
+            gi = " + ".join(terms) if terms else "0"
+            stmt = f"{dst}[{gi}] = ({self.T})gr_lds[{v.addr(idx)}];"
+            self.emit(f"if ({' && '.join(conds)}) {stmt}" if conds else stmt)
+        self.elem_loop(v.shape, body)
+        self.sync()
+
+    def _bcast_shape(self, views):
+        rank = len(views[0].shape)
+        if any(len(v.shape) != rank for v in views):
+            raise UnsupportedProgram("elementwise operands of different rank")
+        out = []
+        for d in range(rank):
+            ns = {v.shape[d] for v in views if v.shape[d] != 1}
+            if len(ns) > 1:
+                raise UnsupportedProgram(f"elementwise shape mismatch on dim {d}: {[v.shape for v in views]}")
+            out.append(ns.pop() if ns else 1)
+        return out
+
+    def gen_compute(self, c: Compute):
+        op = c.op
+        if op in ELEMENTWISE_OPS:
+            ins = [self.view(i) for i in c.inputs]
+            out_shape = self._bcast_shape(ins)
+            wide = max(ins, key=lambda v: (len(v.axes), _prod(v.shape)))
+            axes = wide.axes
+            base = self.alloc(out_shape)
+
+            def body(idx):
+                a = [f"gr_lds[{v.addr(idx)}]" for v in ins]
+                if op == "causal":
+                    p = axes.index(c.axis)
+                    q = p - 1
+                    if q < 0:
+                        raise UnsupportedProgram("causal needs a query axis before the key axis")
+                    expr = (f"((({wide.origin[p]}) + {idx[p]}) > (({wide.origin[q]}) + {idx[q]})) "
+                            f"? -GR_INF : {a[0]}")
+                else:
+                    expr = _ew_expr(op, a, c.const)
+                self.emit(f"gr_lds[{base} + e] = {expr};")
+            self.elem_loop(out_shape, body)
+            self.sync()
+            self.define(c, base, out_shape, axes, wide.origin)
+        elif op in ROW_REDUCE_OPS:
+            v = self.view(c.inputs[0])
+            p = v.axes.index(c.axis)
+            out_shape = list(v.shape)
+            L = out_shape[p]
+            out_shape[p] = 1
+            base = self.alloc(out_shape)
+            self.emit_rowreduce(v, p, L, out_shape, base, op, None)
+            self.sync()
+            org = list(v.origin)
+            org[p] = "0"
+            self.define(c, base, out_shape, v.axes, org)
+        elif op in ("matmul", "softmax_matmul"):
+            a, b = self.view(c.inputs[0]), self.view(c.inputs[1])
+            out_shape = self._mm_shape(a, b)
+            base = self.alloc(out_shape)
+            if op == "matmul":
+                self.emit_matmul(a, b, out_shape, base, accumulate=False)
+            else:
+                self.emit_softmax_matmul_full(a, b, out_shape, base)
+            self.sync()
+            self.define(c, base, out_shape, _value_axes(c), a.origin[:-1] + [b.origin[-1]])
+        else:
+            raise UnsupportedProgram(f"op {op!r}")
+
+    def _mm_shape(self, a, b):
+        if len(a.shape) != len(b.shape) or len(a.shape) < 2:
+            raise UnsupportedProgram("matmul operand ranks")
+        if a.shape[-1] != b.shape[-2]:
+            raise UnsupportedProgram(f"matmul contraction mismatch {a.shape} x {b.shape}")
+        batch = []
+        for x, y in zip(a.shape[:-2], b.shape[:-2]):
+            if x != y and 1 not in (x, y):
+                raise UnsupportedProgram("matmul batch mismatch")
+            batch.append(max(x, y))
+        return batch + [a.shape[-2], b.shape[-1]]
+
+    def emit_matmul(self, a, b, out_shape, base, accumulate):
+        K = a.shape[-1]
+        r = len(out_shape)
+        self.emit(f"// {'mma: acc += A @ B' if accumulate else 'matmul: C = A @ B'} (K = {K})")
+
+        def body(idx):
+            ai = idx[:r - 2] + [idx[r - 2], "k"]
+            bi = idx[:r - 2] + ["k", idx[r - 1]]
+            self.emit("float s = 0.f;")
+            self.emit(f"for (int k = 0; k < {K}; ++k) s = fmaf(gr_lds[{a.addr(ai)}], gr_lds[{b.addr(bi)}], s);")
+            self.emit(f"gr_lds[{base} + e] {'+' if accumulate else ''}= s;")
+        self.elem_loop(out_shape, body)
+
+    def emit_rowreduce(self, v, p, L, out_shape, base, op, acc_mode):
+        init = "-GR_INF" if op == "rowmax" else "0.f"
+        comb = "fmaxf(r, x)" if op == "rowmax" else "r + x"
+
+        def body(idx):
+            ii = list(idx)
+            ii[p] = "k"
+            self.emit(f"float r = {init};")
+            self.emit(f"for (int k = 0; k < {L}; ++k) {{ const float x = gr_lds[{v.addr(ii)}]; r = {comb}; }}")
+            if acc_mode is None:
+                self.emit(f"gr_lds[{base} + e] = r;")
+            elif op == "rowmax":
+                self.emit(f"gr_lds[{base} + e] = fmaxf(gr_lds[{base} + e], r);")
+            else:
+                self.emit(f"gr_lds[{base} + e] += r;")
+        self.elem_loop(out_shape, body)
+
+    def emit_softmax_matmul_full(self, a, b, out_shape, base):
+        """softmax over the last axis of a, then @ b, in one pass per output."""
+        K = a.shape[-1]
+        r = len(out_shape)
+
+        def body(idx):
+            ai = idx[:r - 2] + [idx[r - 2], "k"]
+            bi = idx[:r - 2] + ["k", idx[r - 1]]
+            self.emit("float m = -GR_INF;")
+            self.emit(f"for (int k = 0; k < {K}; ++k) m = fmaxf(m, gr_lds[{a.addr(ai)}]);")
+            self.emit("if (m == -GR_INF) m = 0.f;")
+            self.emit("float l = 0.f, s = 0.f;")
+            self.emit(f"for (int k = 0; k < {K}; ++k) {{ const float p = __expf(gr_lds[{a.addr(ai)}] - m); "
+                      f"l += p; s = fmaf(p, gr_lds[{b.addr(bi)}], s); }}")
+            self.emit(f"gr_lds[{base} + e] = s / l;")
+        self.elem_loop(out_shape, body)
+
+    # -- reduction loops -----------------------------------------------------
+    def gen_reduction(self, rl: ReductionLoop):
+        ext = None
+        for ld in list(_loads_feeding(rl)) + list(_iter_loads(rl.body)):
+            if rl.axis in ld.index:
+                ext = self.p.tensors[ld.source][ld.index.index(rl.axis)]
+                break
+        if ext is None:
+            raise UnsupportedProgram(f"reduction axis {rl.axis!r} not found in any load")
+        if ext % rl.tile:
+            raise UnsupportedProgram(f"reduction tile {rl.tile} does not divide {ext}")
+        accs = {}
+        for p in rl.partials:
+            if not isinstance(p, Compute) or p.op not in ("matmul", "rowmax", "rowsum", "softmax_matmul"):
+                raise UnsupportedProgram("unsupported reduction partial")
+            accs[id(p)] = {"op": p.op, "node": p, "base": None}
+        lv = self.loopvar(rl)
+        # accumulators are allocated lazily at the first partial update (their
+        # shape is known then); allocation/initialisation is hoisted before the loop
+        init_mark = len(self.lines)
+        loop_start = self.pos
+        self.emit(f"for (int {lv} = 0; {lv} < {ext // rl.tile}; ++{lv}) {{")
+        self.ind += 1
+        self.loops.append(rl)
+        saved = self.scope.get(rl.axis)
+        self.scope[rl.axis] = lv
+        self.gen_body(rl.body, partial_acc=accs)
+        self.loops.pop()
+        if saved is None:
+            self.scope.pop(rl.axis, None)
+        else:
+            self.scope[rl.axis] = saved
+        self.ind -= 1
+        self.emit("}")
+        self.step()
+        loop_end = self.pos
+        # values read inside the loop but made before it stay live for the
+        # whole loop (the next iteration reads them again); accumulators are
+        # live from their initialisation before the loop
+        for b in self.bufs.values():
+            if b["def"] < loop_start <= b["last"]:
+                b["last"] = max(b["last"], loop_end)
+        for p in rl.partials:
+            a = accs[id(p)]
+            for key in ("base", "m", "l", "alpha"):
+                if a.get(key) is not None:
+                    bb = self.bufs[a[key]]
+                    bb["def"] = min(bb["def"], loop_start)
+                    bb["last"] = max(bb["last"], loop_end)
+        # initialisation code, inserted before the loop
+        init = []
+        for p in rl.partials:
+            a = accs[id(p)]
+            if a["base"] is None:
+                raise UnsupportedProgram("reduction partial never evaluated")
+            E = _prod(a["shape"])
+            pad = "  " * self.ind
+            if a["op"] == "softmax_matmul":
+                R = _prod(a["shape"][:-1])
+                init.append(f"{pad}for (int e = threadIdx.x; e < {E}; e += {NT}) gr_lds[{a['base']} + e] = 0.f;")
+                init.append(f"{pad}for (int e = threadIdx.x; e < {R}; e += {NT}) {{ gr_lds[{a['m']} + e] = -GR_INF; "
+                            f"gr_lds[{a['l']} + e] = 0.f; }}")
+            else:
+                v = "-GR_INF" if a["op"] == "rowmax" else "0.f"
+                init.append(f"{pad}for (int e = threadIdx.x; e < {E}; e += {NT}) gr_lds[{a['base']} + e] = {v};")
+        init.append("  " * self.ind + "__syncthreads();")
+        self.lines[init_mark:init_mark] = init
+        # finalise (online softmax -> o / l) and publish the values
+        for p in rl.partials:
+            a = accs[id(p)]
+            if a["op"] == "softmax_matmul":
+                E = _prod(a["shape"])
+                N = a["shape"][-1]
+                self.emit(f"for (int e = threadIdx.x; e < {E}; e += {NT}) gr_lds[{a['base']} + e] /= gr_lds[{a['l']} + e / {N}];")
+                self.sync()
+            self.define(p, a["base"], a["shape"], a["axes"], a["origin"])
+        self.vals[id(rl)] = self.vals[id(rl.partials[0])]
+
+    def gen_partial(self, c: Compute, a: dict):
+        op = c.op
+        for key in ("base", "m", "l", "alpha"):
+            if a.get(key) is not None:
+                self.touch(a[key])
+        if op == "matmul":
+            x, y = self.view(c.inputs[0]), self.view(c.inputs[1])
+            shape = self._mm_shape(x, y)
+            self._acc_alloc(a, shape, _value_axes(c), x.origin[:-1] + [y.origin[-1]])
+            self.emit_matmul(x, y, shape, a["base"], accumulate=True)
+        elif op in ROW_REDUCE_OPS:
+            v = self.view(c.inputs[0])
+            p = v.axes.index(c.axis)
+            shape = list(v.shape)
+            L = shape[p]
+            shape[p] = 1
+            org = list(v.origin)
+            org[p] = "0"
+            self._acc_alloc(a, shape, v.axes, org)
+            self.emit_rowreduce(v, p, L, shape, a["base"], op, acc_mode=True)
+        elif op == "softmax_matmul":
+            s, v = self.view(c.inputs[0]), self.view(c.inputs[1])
+            shape = self._mm_shape(s, v)
+            first = a["base"] is None
+            self._acc_alloc(a, shape, _value_axes(c), s.origin[:-1] + [v.origin[-1]])
+            if first:
+                R = _prod(shape[:-1])
+                a["m"] = self.alloc([R])
+                a["l"] = self.alloc([R])
+                a["alpha"] = self.alloc([R])
+            self.emit_online_softmax(s, v, shape, a)
+        else:
+            raise UnsupportedProgram(f"partial op {op!r}")
+        self.sync()
+        self.vals[id(c)] = (a["base"], tuple(a["shape"]), a["axes"], len(self.loops), a["origin"])
+
+    def _acc_alloc(self, a, shape, axes, origin):
+        if a["base"] is None:
+            a["base"] = self.alloc(shape)
+            a["shape"] = tuple(shape)
+            a["axes"] = list(axes)
+            # an accumulator never spans its loop's axis: its origin is loop-invariant
+            a["origin"] = list(origin)
+        elif tuple(shape) != a["shape"]:
+            raise UnsupportedProgram("partial shape changes between iterations")
+
+    def emit_online_softmax(self, s, v, shape, a):
+        K = s.shape[-1]
+        N = shape[-1]
+        rshape = list(shape[:-1]) + [1]
+        r = len(shape)
+
+        def rows(idx):
+            si = idx[:r - 1] + ["k"]
+            self.emit("float mt = -GR_INF;")
+            self.emit(f"for (int k = 0; k < {K}; ++k) mt = fmaxf(mt, gr_lds[{s.addr(si)}]);")
+            self.emit(f"const float mo = gr_lds[{a['m']} + e];")
+            self.emit("const float mn = fmaxf(mo, mt);")
+            self.emit("const float ms = (mn == -GR_INF) ? 0.f : mn;")
+            self.emit("const float al = __expf(mo - ms);")
+            self.emit("float ls = 0.f;")
+            self.emit(f"for (int k = 0; k < {K}; ++k) ls += __expf(gr_lds[{s.addr(si)}] - ms);")
+            self.emit(f"gr_lds[{a['m']} + e] = mn; gr_lds[{a['alpha']} + e] = al;")
+            self.emit(f"gr_lds[{a['l']} + e] = gr_lds[{a['l']} + e] * al + ls;")
+        self.elem_loop(rshape, rows)
+        self.sync()
+
+        def outs(idx):
+            si = idx[:r - 1] + ["k"]
+            vi = idx[:r - 2] + ["k", idx[r - 1]]
+            self.emit(f"const int row = e / {N};")
+            self.emit(f"const float mn = gr_lds[{a['m']} + row];")
+            self.emit("const float ms = (mn == -GR_INF) ? 0.f : mn;")
+            self.emit("float acc = 0.f;")
+            self.emit(f"for (int k = 0; k < {K}; ++k) acc = fmaf(__expf(gr_lds[{s.addr(si)}] - ms), gr_lds[{v.addr(vi)}], acc);")
+            self.emit(f"gr_lds[{a['base']} + e] = gr_lds[{a['base']} + e] * gr_lds[{a['alpha']} + row] + acc;")
+        self.elem_loop(shape, outs)
+
+    # -- kernel ----------------------------------------------------------------
+    def render(self) -> tuple:
+        loop, p = self.loop, self.p
+        g_out = p.tensors[loop.out]
+        grid = [_cdiv(g, t) for g, t in zip(g_out, loop.tile_shape)]
+        kname = f"{_cname(loop.out)}_kernel"
+        args = _loop_tensors(loop)
+        if args.count(loop.out) > 1:
+            raise UnsupportedProgram(f"stage {loop.out} reads its own output")
+        # grid decode (row-major, last output dim fastest)
+        self.emit("int bid = blockIdx.x;")
+        for d in range(len(grid) - 1, -1, -1):
+            var = f"b_{_cname(loop.index_vars[d])}"
+            if grid[d] == 1:
+                self.emit(f"const int {var} = 0;")
+            else:
+                self.emit(f"const int {var} = bid % {grid[d]}; bid /= {grid[d]};")
+            self.scope[loop.index_vars[d]] = var
+        self.gen_body(loop.body)
+        consts = self.assign_lds()
+        if self.nfl * 4 > LDS_LIMIT:
+            raise LdsOverflow(loop.out, self.nfl * 4)
+        params = ", ".join(f"{'const ' if a != loop.out else ''}{self.T}* __restrict__ {_cname(a)}" for a in args)
+        code = [f"// stage {loop.out}: generic LDS-tile kernel, tile {tuple(loop.tile_shape)}, "
+                f"{self.nfl * 4} B LDS",
+                f'extern "C" __global__ __launch_bounds__({NT}) void {kname}({params}) {{',
+                f"  extern __shared__ __attribute__((aligned(16))) float gr_lds[];"]
+        code += consts
+        code += self.lines
+        code.append("}")
+        return "\n".join(code) + "\n", {"kernel": kname, "grid": [_prod(grid), 1, 1], "block": [NT, 1, 1],
+                                          "lds": self.nfl * 4, "args": args, "lowering": "generic"}
+
+
+def _ew_expr(op, a, const):
+    if op == "add":
+        return f"{a[0]} + {a[1]}"
+    if op == "sub":
+        return f"{a[0]} - {a[1]}"
+    if op == "mul":
+        return f"{a[0]} * {a[1]}"
+    if op == "div":
+        return f"{a[0]} / {a[1]}"
+    if op == "relu":
+        return f"fmaxf({a[0]}, 0.f)"
+    if op == "exp":
+        return f"__expf({a[0]})"
+    if op == "sqrt":
+        return f"sqrtf({a[0]})"
+    if op == "mulc":
+        return f"{a[0]} * {_flt(const)}"
+    if op == "addc":
+        return f"{a[0]} + {_flt(const)}"
+    if op == "silu":
+        return f"{a[0]} / (1.f + __expf(-{a[0]}))"
+    raise UnsupportedProgram(f"op {op!r}")
+
+
+# ---------------------------------------------------------------------------
+# Module
+# ---------------------------------------------------------------------------
+PLAN_TAG = "GR_PLAN"
+
+
+def render_module(program: Program, fn_name: str = "fn") -> str:
+    validate(program)
+    shapes = _infer_program(program)
+    meta = kernel_meta(program, shapes)
+    inputs, inter, outputs = _program_io(program)
+    parts = ['#include "gr_flash_fwd.h"', "",
+             f"// generated from a grammar program: {len(program.body)} stage(s), storage {program.dtype}"]
+    steps = []
+    for loop in program.body:
+        f = _match_flash(loop, program)
+        if f is not None:
+            code, step = _render_flash(loop, program, f)
+        else:
+            code, step = _StageGen(loop, program, shapes).render()
+        parts.append(code)
+        steps.append(step)
+    plan = {"fn": fn_name, "dtype": program.dtype, "inputs": inputs, "intermediates": inter, "outputs": outputs,
+            "tensors": {k: list(v) for k, v in program.tensors.items()}, "steps": steps, "meta": meta}
+    parts.append(f"/*{PLAN_TAG} {json.dumps(plan, sort_keys=True)} {PLAN_TAG}*/")
+    return "\n".join(parts) + "\n"
+
+
+def parse_plan(src: str) -> dict:
+    m = re.search(r"/\*" + PLAN_TAG + r" (.*) " + PLAN_TAG + r"\*/", src, re.S)
+    if not m:
+        raise ValueError("source carries no launch plan")
+    return json.loads(m.group(1))

@@ -1,0 +1,155 @@
+"""Load and run a rendered HIP module (the MI355X counterpart of importing a
+generated cuTile module, grammar/optimization.py:306-318, and of the module
+contract fn(*inputs) + KERNEL_META, bench.py:14-20).
+
+    mod = load_module(emit_module(program))
+    out = mod.fn(*inputs)                   # inputs in sorted-name order
+    ms = mod.time(inputs, warmup, iters)    # hipEvents around the launch plan
+
+Compilation goes through hiprtc (runtime.compile_source) with an in-process
+cache and an on-disk code-object cache keyed by (source hash, toolchain
+version). Intermediates and outputs are allocated once per bound input set
+(the reference reallocates them with cp.zeros on every call,
+kernel_ast.py:1271-1272); they start NaN-filled so an incomplete write shows.
+"""
+from __future__ import annotations
+
+import hashlib
+import os
+import threading
+
+from . import runtime as rt
+from .hip_backend import parse_plan
+
+_mem_cache: dict = {}
+_lock = threading.Lock()
+
+
+def cache_dir() -> str | None:
+    d = os.environ.get("GR_CACHE_DIR", os.path.join(os.path.expanduser("~"), ".cache", "gr_hip"))
+    if d.lower() in ("", "0", "off", "none"):
+        return None
+    return d
+
+
+def source_key(src: str) -> str:
+    h = hashlib.sha256()
+    h.update(rt.version().encode())
+    h.update(b"\0")
+    h.update(src.encode())
+    return h.hexdigest()[:32]
+
+
+def compile_cached(src: str, name: str = "gr_module.hip") -> tuple:
+    """(code object bytes, cache hit?) for `src`."""
+    key = source_key(src)
+    with _lock:
+        code = _mem_cache.get(key)
+    if code is not None:
+        return code, True
+    d = cache_dir()
+    path = os.path.join(d, key + ".co") if d else None
+    if path and os.path.exists(path):
+        with open(path, "rb") as f:
+            code = f.read()
+        with _lock:
+            _mem_cache[key] = code
+        return code, True
+    code = rt.compile_source(src, name)
+    with _lock:
+        _mem_cache[key] = code
+    if path:
+        try:
+            os.makedirs(d, exist_ok=True)
+            tmp = f"{path}.{os.getpid()}.tmp"
+            with open(tmp, "wb") as f:
+                f.write(code)
+            os.replace(tmp, path)
+        except OSError:
+            pass
+    return code, False
+
+
+_TORCH_DT = {"fp32": "float32", "fp16": "float16", "bf16": "bfloat16"}
+
+
+class HipModule:
+    def __init__(self, src: str, code: bytes | None = None):
+        self.src = src
+        self.plan = parse_plan(src)
+        self.KERNEL_META = self.plan["meta"]
+        self.inputs = list(self.plan["inputs"])
+        self.code = code if code is not None else compile_cached(src)[0]
+        self.module = rt.Module(self.code)
+        self.kernels = [self.module.kernel(st["kernel"]) for st in self.plan["steps"]]
+        self._bound = None
+
+    @property
+    def dtype(self):
+        import torch
+        return getattr(torch, _TORCH_DT[self.plan["dtype"]])
+
+    def allocate(self, device="cuda") -> dict:
+        """NaN-filled intermediates and outputs."""
+        import torch
+        out = {}
+        for name in self.plan["intermediates"] + self.plan["outputs"]:
+            out[name] = torch.full(tuple(self.plan["tensors"][name]), float("nan"), dtype=self.dtype, device=device)
+        return out
+
+    def bind(self, tensors: dict) -> rt.Plan:
+        """A launch plan with every stage's tensor arguments bound."""
+        steps = []
+        for st, k in zip(self.plan["steps"], self.kernels):
+            args = []
+            for a in st["args"]:
+                t = tensors[a]
+                if tuple(t.shape) != tuple(self.plan["tensors"][a]) or t.dtype != self.dtype or not t.is_contiguous():
+                    raise ValueError(f"tensor {a}: need contiguous {self.plan['tensors'][a]} {self.dtype}, "
+                                     f"got {tuple(t.shape)} {t.dtype}")
+                args.append(t.data_ptr())
+            steps.append((k, st["grid"], st["block"], st["lds"], args))
+        return rt.Plan(steps)
+
+    def _check_inputs(self, inputs):
+        if len(inputs) != len(self.inputs):
+            raise ValueError(f"expected inputs {self.inputs}")
+        for n, t in zip(self.inputs, inputs):
+            if not t.is_cuda:
+                raise ValueError(f"input {n} must be a GPU tensor (no CPU path)")
+
+    def fn(self, *inputs):
+        """Run the module on `inputs` (sorted-name order) and return the output
+        (or a tuple of outputs)."""
+        self._check_inputs(inputs)
+        tensors = dict(zip(self.inputs, inputs))
+        tensors.update(self.allocate(inputs[0].device))
+        self.bind(tensors).run()
+        outs = [tensors[o] for o in self.plan["outputs"]]
+        return outs[0] if len(outs) == 1 else tuple(outs)
+
+    __call__ = fn
+
+    def time(self, inputs, warmup: int = 1, iters: int = 3, mode: int = rt.GR_TIME_MIN) -> float:
+        """ms per run of the whole plan, hipEvents on the current stream:
+        GR_TIME_MIN = min over per-run event pairs (the descent loss,
+        grammar/optimization.py:284-300); GR_TIME_BATCH = mean over one pair
+        around `iters` runs (bench.py:55-61)."""
+        self._check_inputs(inputs)
+        tensors = dict(zip(self.inputs, inputs))
+        tensors.update(self.allocate(inputs[0].device))
+        plan = self.bind(tensors)
+        plan.run()
+        return plan.time(max(0, warmup - 1), iters, mode)
+
+    def run_with(self, inputs) -> dict:
+        """Run once and return every tensor (inputs, intermediates, outputs)."""
+        self._check_inputs(inputs)
+        tensors = dict(zip(self.inputs, inputs))
+        tensors.update(self.allocate(inputs[0].device))
+        self.bind(tensors).run()
+        return tensors
+
+
+def load_module(src: str) -> HipModule:
+    return HipModule(src)
