@@ -13,10 +13,7 @@ import os
 import numpy as np
 import pytest
 
-from grammar.kernel_ast import (
-    Program, ParallelLoop, Load, Store, Compute, ReductionLoop, program_flops, peak_tile_bytes,
-    structural_key, validate,
-)
+from grammar.kernel_ast import program_flops, peak_tile_bytes, program_from_key, structural_key, validate
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 RECORDS = json.load(open(os.path.join(HERE, "golden", "reference_runs.json")))["records"]
@@ -24,53 +21,6 @@ RECORDS = json.load(open(os.path.join(HERE, "golden", "reference_runs.json")))["
 
 def _tuplify(x):
     return tuple(_tuplify(i) for i in x) if isinstance(x, list) else x
-
-
-def program_from_key(key) -> Program:
-    """Inverse of structural_key: body statements in order; a Compute/Store/
-    partial operand refers to the most recent node with that key in the
-    current scope chain."""
-    key = _tuplify(key)
-    assert key[0] == "Program"
-    tensors = {name: tuple(shape) for name, shape in key[1]}
-
-    def build_body(keys, scopes):
-        body = []
-        scopes = scopes + [[]]
-
-        def lookup(k):
-            for sc in reversed(scopes):
-                for kk, node in reversed(sc):
-                    if kk == k:
-                        return node
-            raise KeyError(f"operand {k[:2]} not defined before use")
-
-        for k in keys:
-            kind = k[0]
-            if kind == "Load":
-                node = Load(k[1], list(k[2]))
-            elif kind == "Compute":
-                node = Compute(k[1], [lookup(i) for i in k[4]], axis=k[2], const=k[3])
-            elif kind == "Store":
-                node = Store(k[1], lookup(k[3]), list(k[2]))
-            elif kind == "ReductionLoop":
-                inner, inner_scope = build_body(k[3], scopes)
-                parts = []
-                for pk in k[4]:
-                    parts.append(next(n for kk, n in reversed(inner_scope) if kk == pk))
-                node = ReductionLoop(k[1], k[2], inner, partials=parts)
-            else:
-                raise ValueError(kind)
-            scopes[-1].append((k, node))
-            body.append(node)
-        return body, scopes[-1]
-
-    stages = []
-    for sk in key[2]:
-        assert sk[0] == "ParallelLoop"
-        body, _ = build_body(sk[4], [])
-        stages.append(ParallelLoop(sk[1], tuple(sk[2]), tuple(sk[3]), body))
-    return Program(tensors, stages)
 
 
 def test_fixture_count():
