@@ -46,10 +46,12 @@ class UnsupportedProgram(Exception):
 
 
 class LdsOverflow(UnsupportedProgram):
-    """A stage needs more LDS than one gfx950 workgroup has."""
+    """Stages need more LDS than one gfx950 workgroup has. `need` is the sum
+    over all overflowing stages of their excess bytes (each over-budget stage
+    contributes, so shrinking any one of them lowers it)."""
 
     def __init__(self, stage, need):
-        super().__init__(f"stage {stage}: needs {need} bytes of LDS > {LDS_LIMIT}")
+        super().__init__(f"stage(s) {stage}: {need} bytes of LDS beyond {LDS_LIMIT} per workgroup")
         self.need = need
 
 
@@ -697,7 +699,7 @@ class _StageGen:
         self.gen_body(loop.body)
         consts = self.assign_lds()
         if self.nfl * 4 > LDS_LIMIT:
-            raise LdsOverflow(loop.out, self.nfl * 4)
+            raise LdsOverflow(loop.out, self.nfl * 4 - LDS_LIMIT)
         params = ", ".join(f"{'const ' if a != loop.out else ''}{self.T}* __restrict__ {_cname(a)}" for a in args)
         code = [f"// stage {loop.out}: generic LDS-tile kernel, tile {tuple(loop.tile_shape)}, "
                 f"{self.nfl * 4} B LDS",
@@ -748,18 +750,32 @@ def render_module(program: Program, fn_name: str = "fn") -> str:
     parts = ['#include "gr_flash_fwd.h"', "",
              f"// generated from a grammar program: {len(program.body)} stage(s), storage {program.dtype}"]
     steps = []
+    over, excess = [], 0
     for loop in program.body:
         f = _match_flash(loop, program)
-        if f is not None:
-            code, step = _render_flash(loop, program, f)
-        else:
-            code, step = _StageGen(loop, program, shapes).render()
+        try:
+            if f is not None:
+                code, step = _render_flash(loop, program, f)
+            else:
+                code, step = _StageGen(loop, program, shapes).render()
+        except LdsOverflow as e:
+            over.append(loop.out)
+            excess += e.need
+            continue
         parts.append(code)
         steps.append(step)
+    if over:
+        raise LdsOverflow(",".join(over), excess)
     plan = {"fn": fn_name, "dtype": program.dtype, "inputs": inputs, "intermediates": inter, "outputs": outputs,
             "tensors": {k: list(v) for k, v in program.tensors.items()}, "steps": steps, "meta": meta}
     parts.append(f"/*{PLAN_TAG} {json.dumps(plan, sort_keys=True)} {PLAN_TAG}*/")
     return "\n".join(parts) + "\n"
+
+
+def flash_stage_indices(program: Program) -> set:
+    """Indices of the stages that lower to the flash kernel (their working set
+    lives in registers and a fixed LDS ring, not in per-value LDS tiles)."""
+    return {i for i, loop in enumerate(program.body) if _match_flash(loop, program) is not None}
 
 
 def parse_plan(src: str) -> dict:

@@ -51,9 +51,13 @@ class EvalConfig:
     proxy: bool = False                 # dev-only fake score, no GPU
     seed: int = 0
     log: bool = False
-    mem_budget: int = 128 * 1024        # largest single tile (fp32 bytes); gfx950 LDS is 160 KiB
+    mem_budget: int = 128 * 1024        # largest single fp32 tile of a generic stage (gfx950 LDS is
+                                        # 160 KiB per workgroup); flash-lowered stages are exempt
     compile_timeout: float = 60.0       # seconds for one hiprtc compile; 0 disables
-    max_compile_risk: int = 256         # straight-line contraction extent gate; 0 disables
+    max_compile_risk: int = 0           # straight-line contraction extent gate; 0 disables. The
+                                        # reference gates ptxas compile-time blow-up (default 256);
+                                        # hiprtc compiles every stage form in well under a second
+                                        # (loops are not unrolled), so it is off here
     repairable: bool = True             # memory check soft (penalty) vs hard precondition
     reduction_tile_default: int = 32    # tile of a fresh subtile_reduction loop
     check: bool = True                  # tolerance-check every compiled variant
@@ -141,7 +145,10 @@ class Evaluator:
         """Static penalty (memory / compile risk), or None if the program may be compiled."""
         cfg = self.cfg
         if cfg.mem_budget:
+            from .hip_backend import flash_stage_indices
             per = kernel_peak_tile_bytes(program)
+            for i in flash_stage_indices(program):
+                per[i] = 0
             if per and max(per) > cfg.mem_budget:
                 excess = sum(max(0, k - cfg.mem_budget) for k in per)
                 return MEM_PENALTY_BASE + excess / 1024.0
