@@ -93,7 +93,7 @@ __device__ __forceinline__ float gr_xor32(float v) {
   return __shfl_xor(v, 32, 64);
 }
 
-// 2^x on the transcendental unit (v_exp_f32). Inputs here are <= 0 or -inf.
+// 2^x on the transcendental unit (v_exp_f32); overflows to +inf, -inf gives 0.
 __device__ __forceinline__ float gr_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Pack two storage-type values into one dword (low = a, high = b).

@@ -1,0 +1,95 @@
+// gr_gemm.hip -- prebuilt instances of the MFMA GEMM with fused epilogue
+// (gr_gemm.h) behind gr_gemm(), and the two-GEMM MLP block gr_mlp_fwd().
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "gr_gemm.h"
+#include "gr_host.h"
+#include "grammar_rt.h"
+
+namespace {
+
+template <class T, int BM, int BN, int BK, int WGM, int WGN, bool KM, int EPI>
+int launch_gemm(const gr_gemm_args& a, int batch, hipStream_t st) {
+  typedef gr_gemm_cfg<BM, BN, BK, WGM, WGN> G;
+  if (a.M % BM || a.N % BN || a.K % BK)
+    return gr::fail(GR_E_ARG, "gr_gemm: M=%d N=%d K=%d must be multiples of the tile %dx%dx%d", a.M, a.N, a.K, BM,
+                    BN, BK);
+  const long long nblk = (long long)(a.M / BM) * (a.N / BN);
+  if (nblk <= 0 || nblk > 0x7fffffffLL || batch > 65535)
+    return gr::fail(GR_E_ARG, "gr_gemm: grid (%lld tiles, batch %d) out of range", nblk, batch);
+  hipLaunchKernelGGL((gr_gemm_kernel<T, BM, BN, BK, WGM, WGN, KM, EPI>), dim3((unsigned)nblk, (unsigned)batch),
+                     dim3(G::NT), G::LDS, st, a);
+  return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_gemm launch");
+}
+
+// (block_m, block_n) -> (k tile, wave grid) compiled into the library.
+template <class T, bool KM, int EPI>
+int dispatch_tile(const gr_gemm_args& a, int batch, int bm, int bn, hipStream_t st) {
+  if (bm == 0) bm = 256;
+  if (bn == 0) bn = 256;
+  if (bm == 128 && bn == 128) return launch_gemm<T, 128, 128, 64, 2, 2, KM, EPI>(a, batch, st);
+  if (bm == 256 && bn == 128) return launch_gemm<T, 256, 128, 32, 2, 2, KM, EPI>(a, batch, st);
+  if (bm == 128 && bn == 256) return launch_gemm<T, 128, 256, 32, 2, 2, KM, EPI>(a, batch, st);
+  if (bm == 256 && bn == 256) return launch_gemm<T, 256, 256, 64, 2, 4, KM, EPI>(a, batch, st);
+  return gr::fail(GR_E_ARG, "gr_gemm: unsupported tile (block_m=%d, block_n=%d)", bm, bn);
+}
+
+template <class T>
+int dispatch(const gr_gemm_args& a, int batch, bool km, int epi, int bm, int bn, hipStream_t st) {
+#define GR_CASE(K, E) \
+  if (km == K && epi == E) return dispatch_tile<T, K, E>(a, batch, bm, bn, st);
+  GR_CASE(false, GR_EPI_NONE)
+  GR_CASE(false, GR_EPI_RELU)
+  GR_CASE(false, GR_EPI_SILU)
+  GR_CASE(true, GR_EPI_NONE)
+  GR_CASE(true, GR_EPI_RELU)
+  GR_CASE(true, GR_EPI_SILU)
+#undef GR_CASE
+  return gr::fail(GR_E_ARG, "gr_gemm: epilogue %d unsupported", epi);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+extern "C" int gr_gemm(const void* a, const void* b, void* c, int dtype, int batch, int M, int N, int K,
+                       const long long* a_strides, const long long* b_strides, const long long* c_strides,
+                       int b_kmajor, int epilogue, float alpha, int block_m, int block_n, void* stream) {
+  if (!a || !b || !c || !a_strides || !b_strides || !c_strides) return gr::fail(GR_E_ARG, "gr_gemm: null argument");
+  if (batch <= 0 || M <= 0 || N <= 0 || K <= 0) return gr::fail(GR_E_ARG, "gr_gemm: sizes must be positive");
+  if (!aligned16(a) || !aligned16(b) || !aligned16(c))
+    return gr::fail(GR_E_ARG, "gr_gemm: base pointers must be 16-byte aligned");
+  const long long* all[3] = {a_strides, b_strides, c_strides};
+  for (int t = 0; t < 3; ++t)
+    for (int i = 0; i < 2; ++i)
+      if (all[t][i] < 0 || (all[t][i] % 8) != 0)
+        return gr::fail(GR_E_ARG, "gr_gemm: strides must be non-negative multiples of 8 elements");
+  // 32-bit per-thread offsets inside one tile walk: the rows a tile spans
+  if (a_strides[1] > 0x3fffffffLL / 256 || b_strides[1] > 0x3fffffffLL / 256)
+    return gr::fail(GR_E_ARG, "gr_gemm: row strides too large");
+  gr_gemm_args g;
+  g.a = a;
+  g.b = b;
+  g.c = c;
+  g.a_sb = a_strides[0]; g.a_sm = a_strides[1];
+  g.b_sb = b_strides[0]; g.b_s = b_strides[1];
+  g.c_sb = c_strides[0]; g.c_sm = c_strides[1];
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.alpha = alpha;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == GR_F16) return dispatch<_Float16>(g, batch, b_kmajor != 0, epilogue, block_m, block_n, st);
+  if (dtype == GR_BF16) return dispatch<__bf16>(g, batch, b_kmajor != 0, epilogue, block_m, block_n, st);
+  return gr::fail(GR_E_ARG, "gr_gemm: dtype %d unsupported (GR_F16 or GR_BF16)", dtype);
+}
+
+extern "C" int gr_mlp_fwd(const void* x, const void* w1, const void* w2, void* h, void* y, int dtype, int M,
+                          int D, int F, int block_m, int block_n, void* stream) {
+  const long long xs[2] = {0, D}, w1s[2] = {0, F}, hs[2] = {0, F}, w2s[2] = {0, D}, ys[2] = {0, D};
+  int rc = gr_gemm(x, w1, h, dtype, 1, M, F, D, xs, w1s, hs, 0, GR_EPI_SILU, 1.0f, block_m, block_n, stream);
+  if (rc != 0) return rc;
+  return gr_gemm(h, w2, y, dtype, 1, M, D, F, hs, w2s, ys, 0, GR_EPI_NONE, 1.0f, block_m, block_n, stream);
+}

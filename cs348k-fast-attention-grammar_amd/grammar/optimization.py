@@ -130,9 +130,28 @@ class Evaluator:
             if self._gated(p) is not None:
                 continue
             if self._pool is None:
-                self._pool = ThreadPoolExecutor(max_workers=max(1, self.cfg.compile_workers))
+                self._pool = self._new_pool()
             from .hip_module import compile_cached
             self._futures[key] = self._pool.submit(compile_cached, src)
+
+    def _require_device(self):
+        """A missing GPU is an error of the run, not a loss of the variant."""
+        if getattr(self, "_device_ok", False):
+            return
+        import torch
+        from . import runtime as rt
+        rt.lib()
+        if not torch.cuda.is_available():
+            raise RuntimeError("Evaluator: no HIP device visible to torch; timed evaluation needs a GPU "
+                               "(use proxy=True on a CPU-only host)")
+        self._device_ok = True
+
+    def _new_pool(self):
+        # load the runtime (and torch's HIP runtime before it) on this thread,
+        # not inside a compile worker
+        from . import runtime as rt
+        rt.lib()
+        return ThreadPoolExecutor(max_workers=max(1, self.cfg.compile_workers))
 
     def stats(self) -> dict:
         el = max(1e-9, time.time() - self.t_start)
@@ -186,6 +205,7 @@ class Evaluator:
             if self.cfg.log:
                 print(f"{self._tag} static gate -> penalty {g:.0f} (not compiled)", flush=True)
             return g
+        self._require_device()
         try:
             return self._run_gpu(program, key, src, t_emit)
         except _CompileTimeout:
@@ -202,7 +222,7 @@ class Evaluator:
         fut = self._futures.pop(key, None)
         if fut is None:
             if self._pool is None:
-                self._pool = ThreadPoolExecutor(max_workers=max(1, self.cfg.compile_workers))
+                self._pool = self._new_pool()
             fut = self._pool.submit(compile_cached, src)
         try:
             code, hit = fut.result(timeout=self.cfg.compile_timeout or None)

@@ -43,6 +43,7 @@ _lock = threading.Lock()
 
 _u32x3 = ctypes.c_uint32 * 3
 _ll3 = ctypes.c_longlong * 3
+_ll2 = ctypes.c_longlong * 2
 
 
 def lib() -> ctypes.CDLL:
@@ -57,6 +58,10 @@ def lib() -> ctypes.CDLL:
             raise RuntimeError(
                 f"{LIB_PATH} is missing: build it with `python __graft_entry__.py` "
                 "or build_native.py before using the HIP path")
+        # torch must bring its HIP runtime into the process first: when this
+        # library is loaded first, /opt/rocm's libamdhip64 comes in ahead of
+        # torch's bundled one and torch then reports "No HIP GPUs are available".
+        import torch  # noqa: F401
         L = ctypes.CDLL(LIB_PATH)
         vp, sz, i32, u64p = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.POINTER(ctypes.c_uint64)
         L.gr_last_error.restype = ctypes.c_char_p
@@ -80,6 +85,9 @@ def lib() -> ctypes.CDLL:
         L.gr_attn_fwd.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, _ll3, _ll3, _ll3, _ll3,
                                   i32, i32, ctypes.c_float, i32, i32, vp]
         L.gr_selftest_mfma32.argtypes = [vp, vp, vp, vp]
+        L.gr_gemm.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, _ll2, _ll2, _ll2, i32, i32,
+                              ctypes.c_float, i32, i32, vp]
+        L.gr_mlp_fwd.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp]
         _lib = L
         return L
 
@@ -89,7 +97,7 @@ EXPORTED = (
     "gr_last_error", "gr_version", "gr_device_info", "gr_compile", "gr_free_code",
     "gr_module_load", "gr_module_free", "gr_get_kernel", "gr_launch", "gr_plan_create",
     "gr_plan_set_step", "gr_plan_run", "gr_plan_free", "gr_plan_time", "gr_attn_fwd",
-    "gr_selftest_mfma32",
+    "gr_selftest_mfma32", "gr_gemm", "gr_mlp_fwd",
 )
 
 

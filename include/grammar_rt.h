@@ -113,6 +113,35 @@ int gr_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
                 const long long* v_strides, const long long* o_strides, int k_transposed,
                 int causal, float scale, int block_m, int block_n, void* stream);
 
+/* Batched GEMM with fused epilogue, C[z] = act(alpha * A[z] @ B[z]).
+ * Replaces the grammar's matmul stage (a stage whose body is matmul over a
+ * contraction axis, optionally followed by mulc and relu/silu:
+ * grammar/kernel_ast.py:168-223 EMIT_RULES/CONST_OPS, :826-845 accumulator
+ * and K loop) as rendered for the MLP (run_mlp_search.py:42-127).
+ *  dtype: GR_F16 or GR_BF16 (fp32 accumulate); batch: number of matrices.
+ *  A: [batch][M][K], a_strides = {batch, row}; unit stride along K.
+ *  B: [batch][K][N] (b_kmajor == 0, unit stride along N) or [batch][N][K]
+ *     (b_kmajor != 0, unit stride along K); b_strides = {batch, row}.
+ *  C: [batch][M][N], c_strides = {batch, row}; unit stride along N.
+ *  Strides are in elements, multiples of 8; batch stride 0 broadcasts.
+ *  epilogue: GR_EPI_NONE, GR_EPI_RELU or GR_EPI_SILU, applied to alpha*acc.
+ *  (block_m, block_n) in {(128,128), (256,128), (128,256), (256,256)}
+ *  (0 = 256); M, N and K must be multiples of the tile (k tile 64 for the
+ *  square tiles, 32 otherwise). */
+#define GR_EPI_NONE 0
+#define GR_EPI_RELU 1
+#define GR_EPI_SILU 2
+int gr_gemm(const void* a, const void* b, void* c, int dtype, int batch, int M, int N, int K,
+            const long long* a_strides, const long long* b_strides, const long long* c_strides,
+            int b_kmajor, int epilogue, float alpha, int block_m, int block_n, void* stream);
+
+/* MLP block Y = SiLU(X @ W1) @ W2 as two GEMMs, SiLU fused into the first.
+ * The grammar's MLP program (run_mlp_search.py:42-127, with silu in place of
+ * relu + residual + LayerNorm). X [M][D], W1 [D][F], W2 [F][D], Y [M][D],
+ * all row-major and contiguous; h is caller-provided [M][F] workspace. */
+int gr_mlp_fwd(const void* x, const void* w1, const void* w2, void* h, void* y, int dtype, int M,
+               int D, int F, int block_m, int block_n, void* stream);
+
 /* Self-test of the 32x32x16 MFMA operand/accumulator layout the kernels
  * assume: one wavefront computes D[32][32] = A[32][16] @ B[16][32] (fp16 in,
  * fp32 out, all row-major device buffers). */
