@@ -32,7 +32,7 @@ import re
 from .kernel_ast import (
     Program, ParallelLoop, Load, Store, Compute, ReductionLoop, ROW_REDUCE_OPS, ELEMENTWISE_OPS,
     _infer_program, _resolve_index, _value_axes, _program_io, _loop_tensors, validate, kernel_meta,
-    _loads_feeding, _iter_loads, _axis_global_extent,
+    _loads_feeding, _iter_loads, _axis_global_extent, _contraction_axis,
 )
 
 NT = 256                      # threads per workgroup of generic kernels
@@ -194,6 +194,154 @@ void {kname}({params}) {{
     return code, {"kernel": kname, "grid": [grid, 1, 1], "block": [nt, 1, 1], "lds": lds,
                   "args": args, "lowering": "flash",
                   "tiles": {"block_m": f["BM"], "block_n": f["BN"]}}
+
+
+# ---------------------------------------------------------------------------
+# GEMM lowering
+# ---------------------------------------------------------------------------
+GEMM_ACTS = {"relu": 1, "silu": 2}
+GEMM_WAVES_M = {32: 1, 64: 1, 128: 2, 256: 2}
+GEMM_WAVES_N = {32: 1, 64: 1, 128: 2, 256: 2}
+
+
+def _gemm_waves(bm, bn):
+    wgm, wgn = GEMM_WAVES_M[bm], GEMM_WAVES_N[bn]
+    if bm == 256 and bn == 256:
+        wgn = 4
+    return wgm, wgn
+
+
+def _match_gemm(loop: ParallelLoop, program: Program):
+    """Return the GEMM parameters if `loop` computes act(alpha * A @ B) from two
+    loaded operands (the matmul over its contraction axis, at full extent or
+    in one ReductionLoop, then mulc* and at most one relu/silu), else None."""
+    if program.dtype not in ("fp16", "bf16"):
+        return None
+    stores = [s for s in loop.body if isinstance(s, Store)]
+    if len(stores) != 1 or stores[0].dest != loop.out:
+        return None
+    st = stores[0]
+    x, alpha, act = st.src, 1.0, 0
+    chain = []
+    while isinstance(x, Compute) and x.op in ("mulc", "relu", "silu"):
+        chain.append(x)
+        x = x.inputs[0]
+    for c in reversed(chain):            # innermost first: mulc* then one activation
+        if c.op == "mulc":
+            if act:
+                return None
+            alpha *= float(c.const)
+        else:
+            if act:
+                return None
+            act = GEMM_ACTS[c.op]
+    rl = None
+    if isinstance(x, ReductionLoop):
+        rl = x
+        if len(rl.partials) != 1 or any(isinstance(s, ReductionLoop) for s in rl.body):
+            return None
+        mm = rl.partial
+        if not (isinstance(mm, Compute) and mm.op == "matmul"):
+            return None
+    elif isinstance(x, Compute) and x.op == "matmul":
+        mm = x
+    else:
+        return None
+    aload, bload = mm.inputs
+    if not (isinstance(aload, Load) and isinstance(bload, Load)):
+        return None
+    allowed = {id(st), id(mm), id(aload), id(bload)} | {id(c) for c in chain}
+    if rl is not None:
+        allowed.add(id(rl))
+        if rl.axis != _contraction_axis(mm):
+            return None
+    body = list(loop.body) + (list(rl.body) if rl is not None else [])
+    if any(id(s) not in allowed for s in body):
+        return None
+    T = program.tensors
+    out = T[loop.out]
+    nb = len(out) - 2
+    iv = list(loop.index_vars)
+    if nb < 0 or len(iv) != len(out):
+        return None
+    bax, iax, jax = iv[:nb], iv[nb], iv[nb + 1]
+    kax = _contraction_axis(mm)
+    if st.index != bax + [iax, jax]:
+        return None
+    ash, bsh = T[aload.source], T[bload.source]
+    # A: [lead?, M, K]; B: [lead?, K, N] or K-major [lead?, N, K]; lead == bax or absent
+    def lead_ok(ld, shape):
+        lead = ld.index[:-2]
+        if lead == bax:
+            return tuple(shape[:-2]) == tuple(out[:nb]), True
+        return (len(lead) == 0 or all(shape[d] == 1 for d in range(len(lead)))), False
+    if aload.index[-2:] != [iax, kax]:
+        return None
+    if bload.index[-2:] == [kax, jax]:
+        kmajor = False
+    elif bload.index[-2:] == [jax, kax]:
+        kmajor = True
+    else:
+        return None
+    a_ok, a_batched = lead_ok(aload, ash)
+    b_ok, b_batched = lead_ok(bload, bsh)
+    if not (a_ok and b_ok) or not a_batched and nb > 0 and _prod(out[:nb]) > 1:
+        return None
+    M, K = ash[-2], ash[-1]
+    N = bsh[-2] if kmajor else bsh[-1]
+    if (bsh[-1] if kmajor else bsh[-2]) != K or tuple(out[-2:]) != (M, N):
+        return None
+    tile = loop.tile_shape
+    if any(t != 1 for t in tile[:nb]):
+        return None
+    BM, BN = tile[nb], tile[nb + 1]
+    if BM not in GEMM_WAVES_M or BN not in GEMM_WAVES_N or M % BM or N % BN:
+        return None
+    BK = rl.tile if rl is not None else 64
+    while BK > 16 and 2 * (BM + BN) * BK * 2 > LDS_LIMIT:
+        BK //= 2
+    if BK not in (16, 32, 64, 128) or K % BK:
+        BK = 32 if K % 32 == 0 else (16 if K % 16 == 0 else 0)
+    if not BK or 2 * (BM + BN) * BK * 2 > LDS_LIMIT:
+        return None
+    if M * K % 8 or K * N % 8 or K % 8 or N % 8:
+        return None
+    wgm, wgn = _gemm_waves(BM, BN)
+    batch = _prod(out[:nb])
+    return {"a": aload.source, "b": bload.source, "c": loop.out, "M": M, "N": N, "K": K, "batch": batch,
+            "a_sb": M * K if a_batched else 0, "b_sb": K * N if b_batched else 0, "c_sb": M * N,
+            "kmajor": kmajor, "act": act, "alpha": alpha, "BM": BM, "BN": BN, "BK": BK, "WGM": wgm, "WGN": wgn}
+
+
+def _render_gemm(loop, program, f) -> tuple:
+    T = CTYPE[program.dtype]
+    kname = f"{_cname(loop.out)}_kernel"
+    args = _loop_tensors(loop)
+    params = ", ".join(f"{'const ' if a != loop.out else ''}{T}* __restrict__ {_cname(a)}" for a in args)
+    km = "true" if f["kmajor"] else "false"
+    tpl = f"{T}, {f['BM']}, {f['BN']}, {f['BK']}, {f['WGM']}, {f['WGN']}, {km}, {f['act']}"
+    nt = f["WGM"] * f["WGN"] * 64
+    code = f"""
+// stage {loop.out}: MFMA GEMM {f['M']}x{f['N']}x{f['K']} (x{f['batch']}), tile {f['BM']}x{f['BN']}x{f['BK']}
+extern "C" __global__ __launch_bounds__({nt})
+__attribute__((amdgpu_waves_per_eu(gr_gemm_wpe<{f['BM']}, {f['BN']}, {f['BK']}, {f['WGM']}, {f['WGN']}, {km}>::value)))
+void {kname}({params}) {{
+  extern __shared__ __attribute__((aligned(16))) char gr_gemm_smem[];
+  gr_gemm_args a;
+  a.a = {_cname(f['a'])}; a.b = {_cname(f['b'])}; a.c = {_cname(f['c'])};
+  a.a_sb = {f['a_sb']}LL; a.a_sm = {f['K']};
+  a.b_sb = {f['b_sb']}LL; a.b_s = {f['K'] if f['kmajor'] else f['N']};
+  a.c_sb = {f['c_sb']}LL; a.c_sm = {f['N']};
+  a.M = {f['M']}; a.N = {f['N']}; a.K = {f['K']};
+  a.alpha = {_flt(f['alpha'])};
+  gr_gemm_body<{tpl}>(a, gr_gemm_smem);
+}}
+"""
+    grid = (f["M"] // f["BM"]) * (f["N"] // f["BN"])
+    lds = 2 * (f["BM"] + f["BN"]) * f["BK"] * 2
+    return code, {"kernel": kname, "grid": [grid, f["batch"], 1], "block": [nt, 1, 1], "lds": lds,
+                  "args": args, "lowering": "gemm",
+                  "tiles": {"block_m": f["BM"], "block_n": f["BN"], "block_k": f["BK"]}}
 
 
 # ---------------------------------------------------------------------------
@@ -747,15 +895,18 @@ def render_module(program: Program, fn_name: str = "fn") -> str:
     shapes = _infer_program(program)
     meta = kernel_meta(program, shapes)
     inputs, inter, outputs = _program_io(program)
-    parts = ['#include "gr_flash_fwd.h"', "",
+    parts = ['#include "gr_gemm.h"', "",
              f"// generated from a grammar program: {len(program.body)} stage(s), storage {program.dtype}"]
     steps = []
     over, excess = [], 0
     for loop in program.body:
         f = _match_flash(loop, program)
+        gm = _match_gemm(loop, program) if f is None else None
         try:
             if f is not None:
                 code, step = _render_flash(loop, program, f)
+            elif gm is not None:
+                code, step = _render_gemm(loop, program, gm)
             else:
                 code, step = _StageGen(loop, program, shapes).render()
         except LdsOverflow as e:
@@ -773,9 +924,11 @@ def render_module(program: Program, fn_name: str = "fn") -> str:
 
 
 def flash_stage_indices(program: Program) -> set:
-    """Indices of the stages that lower to the flash kernel (their working set
-    lives in registers and a fixed LDS ring, not in per-value LDS tiles)."""
-    return {i for i, loop in enumerate(program.body) if _match_flash(loop, program) is not None}
+    """Indices of the stages that lower to a hand-tiled MFMA kernel (flash or
+    GEMM): their working set lives in registers and a fixed LDS ring, not in
+    per-value LDS tiles."""
+    return {i for i, loop in enumerate(program.body)
+            if _match_flash(loop, program) is not None or _match_gemm(loop, program) is not None}
 
 
 def parse_plan(src: str) -> dict:

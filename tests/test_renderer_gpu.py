@@ -108,3 +108,72 @@ def test_generic_fp16_attention_matches_rounded_interpreter():
     out = mod.fn(*[torch.from_numpy(ins16[n]).to(dev).half() for n in mod.inputs]).float().cpu().numpy()
     want = run_program(prog, ins16, storage_round=rnd)["O"]
     assert np.allclose(out, want, rtol=2e-3, atol=2e-3)
+
+
+def test_gemm_lowered_attention_stages():
+    """The atomic attention program at fp16: its two matmul stages lower to the
+    MFMA GEMM (S with K given transposed as [d, N], O with V as [N, d]); the
+    softmax stages stay generic. Output against the fp32 oracle."""
+    dev = _cuda()
+    from grammar.hip_module import load_module
+    from grammar.workloads import AttnConfig, attention_inputs
+    import run_attention_search as RS
+    prog = RS.build_attention(256, 64, tile=64, B=2, H=2, dtype="fp16")
+    mod = load_module(emit_module(prog))
+    low = {s["kernel"]: s["lowering"] for s in mod.plan["steps"]}
+    print(f"[gemm-lowered] attention stages {low}", flush=True)
+    assert low["t_S_kernel"] == "gemm" and low["t_O_kernel"] == "gemm"
+    q, kt, v = attention_inputs(AttnConfig("t", 2, 2, 256, 64, "fp16", False), seed=4, k_transposed=True)
+    o = mod.fn(kt.to(dev), q.to(dev), v.to(dev))
+    torch.cuda.synchronize()
+    ref = O.attention(q.float().numpy(), kt.float().numpy(), v.float().numpy(), k_transposed=True)
+    mx, mn = O.errors(o.float().cpu().numpy(), ref)
+    print(f"[gemm-lowered] attention: max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)
+    assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL
+
+
+@pytest.mark.parametrize("dt", ["fp16", "bf16"])
+def test_gemm_lowered_mlp_program(dt):
+    """Y = SiLU(X W1) W2 from the grammar: after merge(h, a) both stages lower
+    to the GEMM, the first with its SiLU epilogue."""
+    dev = _cuda()
+    from grammar.hip_module import load_module
+    import run_mlp_search as RM
+    prog = RM.build_mlp_silu(256, 128, 256, tile=128, subtile_k=64, dtype=dt)
+    prog = R.merge(prog, prog.body[0], prog.body[1])
+    mod = load_module(emit_module(prog))
+    assert [s["lowering"] for s in mod.plan["steps"]] == ["gemm", "gemm"]
+    ins = RM.mlp_inputs(256, 128, 256, dt, seed=2, device=str(dev))
+    y = mod.fn(*[ins[n] for n in mod.inputs])
+    torch.cuda.synchronize()
+    ref = O.mlp_silu(ins["X"].float().cpu().numpy(), ins["W1"].float().cpu().numpy(),
+                     ins["W2"].float().cpu().numpy(), dtype=np.float64)
+    mx, mn = O.errors(y.float().cpu().numpy(), ref)
+    print(f"[gemm-lowered] mlp {dt}: max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)
+    assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL
+    assert np.allclose(RM.verify(prog, "silu"), True)
+
+
+def test_gemm_lowered_batched_with_shared_weight():
+    """A batched [2, 128, 64] operand against one [64, 128] weight (batch
+    stride 0), with a mulc + relu epilogue."""
+    dev = _cuda()
+    from grammar.hip_module import load_module
+    from grammar.kernel_ast import Program, ParallelLoop, Store
+    A, W = Load("A", ["b", "i", "k"]), Load("W", ["k", "j"])
+    mm = Compute("matmul", [A, W])
+    sc = Compute("mulc", [mm], const=0.5)
+    rl = Compute("relu", [sc])
+    prog = Program({"A": (2, 128, 64), "W": (64, 128), "C": (2, 128, 128)},
+                   [ParallelLoop("C", (1, 128, 128), ("b", "i", "j"), [A, W, mm, sc, rl, Store("C", rl, ["b", "i", "j"])])],
+                   "fp16")
+    mod = load_module(emit_module(prog))
+    assert [s["lowering"] for s in mod.plan["steps"]] == ["gemm"]
+    g = torch.Generator("cpu").manual_seed(9)
+    a = torch.randn((2, 128, 64), generator=g).half()
+    w = (torch.randn((64, 128), generator=g) / 8).half()
+    c = mod.fn(a.to(dev), w.to(dev))
+    torch.cuda.synchronize()
+    ref = np.maximum(0.5 * (a.double().numpy() @ w.double().numpy()), 0.0)
+    mx, mn = O.errors(c.float().cpu().numpy(), ref)
+    assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL
