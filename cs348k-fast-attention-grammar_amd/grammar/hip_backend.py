@@ -82,51 +82,97 @@ def _flt(x: float) -> str:
 FLASH_BM = {32: (1, 1), 64: (2, 1), 128: (4, 1), 256: (4, 2)}   # block_m -> (waves, query blocks/wave)
 
 
-def _match_flash(loop: ParallelLoop, program: Program):
-    """Return the flash parameters if `loop` is the flash pattern, else None."""
-    if program.dtype not in ("fp16", "bf16"):
-        return None
-    reds = [s for s in loop.body if isinstance(s, ReductionLoop)]
-    stores = [s for s in loop.body if isinstance(s, Store)]
-    if len(reds) != 1 or len(stores) != 1 or len(reds[0].partials) != 1:
-        return None
-    rl, st = reds[0], stores[0]
-    smm = rl.partial
-    if not (isinstance(smm, Compute) and smm.op == "softmax_matmul" and smm.axis == rl.axis):
-        return None
-    if st.src is not rl or st.dest != loop.out:
-        return None
-    x, vload = smm.inputs
-    if not isinstance(vload, Load):
-        return None
-    inner = {id(s) for s in rl.body}
-    causal, scale = False, 1.0
-    if isinstance(x, Compute) and x.op == "causal":
-        if x.axis != rl.axis or id(x) not in inner:
+FLASH_DEFAULT_BN = {64: 128, 128: 64}    # key tile when the stage does not tile the key axis
+
+
+def _flash_scores(x, scope_ids):
+    """Walk the score operand of a softmax_matmul down to its Q K^T product.
+    Accepts [causal] and [mulc] (either order, at most one each) over a
+    matmul(Load Q, Load KT) that is bare or the sole partial of a
+    ReductionLoop over the head dim. Returns (causal, scale, qload, ktload,
+    nodes) or None; every node must be in `scope_ids`."""
+    causal, scale, nodes = False, 1.0, []
+    seen_mulc = False
+    while isinstance(x, Compute) and x.op in ("causal", "mulc"):
+        if id(x) not in scope_ids:
             return None
-        causal, x = True, x.inputs[0]
-    if isinstance(x, Compute) and x.op == "mulc":
-        if id(x) not in inner:
+        if x.op == "causal":
+            if causal:
+                return None
+            causal = True
+            cax = x.axis
+        else:
+            if seen_mulc:
+                return None
+            seen_mulc, scale = True, float(x.const)
+        nodes.append(x)
+        x = x.inputs[0]
+    if id(x) not in scope_ids:
+        return None
+    dloop = None
+    if isinstance(x, ReductionLoop):
+        dloop = x
+        if len(dloop.partials) != 1 or not all(isinstance(s, (Load, Compute)) for s in dloop.body):
             return None
-        scale, x = float(x.const), x.inputs[0]
-    if isinstance(x, Compute) and x.op == "causal" and not causal:
-        if x.axis != rl.axis or id(x) not in inner:
-            return None
-        causal, x = True, x.inputs[0]
-    if not (isinstance(x, Compute) and x.op == "matmul" and id(x) in inner):
+        nodes.append(dloop)
+        nodes.extend(dloop.body)
+        x = dloop.partial
+    if not (isinstance(x, Compute) and x.op == "matmul"):
+        return None
+    if dloop is not None and (dloop.axis != _contraction_axis(x) or
+                              any(isinstance(s, Compute) and s is not x for s in dloop.body)):
         return None
     qload, ktload = x.inputs
     if not (isinstance(qload, Load) and isinstance(ktload, Load)):
         return None
-    # other statements must be exactly these loads/computes
-    allowed = {id(rl), id(st), id(qload), id(ktload), id(vload), id(smm), id(x)}
-    chain = smm.inputs[0]
-    while isinstance(chain, Compute) and chain is not x:
-        allowed.add(id(chain))
-        chain = chain.inputs[0]
-    for s in list(loop.body) + list(rl.body):
-        if id(s) not in allowed:
+    nodes += [x, qload, ktload]
+    return causal, scale, qload, ktload, nodes
+
+
+def _match_flash(loop: ParallelLoop, program: Program):
+    """Return the flash parameters if `loop` is one attention stage, else None:
+    O = softmax_matmul(x, V) over the key axis j -- bare (full key range) or
+    the sole partial of a ReductionLoop over j -- with x the scaled and
+    optionally causally masked Q K^T of `_flash_scores`, and nothing else."""
+    if program.dtype not in ("fp16", "bf16"):
+        return None
+    stores = [s for s in loop.body if isinstance(s, Store)]
+    if len(stores) != 1 or stores[0].dest != loop.out:
+        return None
+    st = stores[0]
+    src = st.src
+    rl = None
+    if isinstance(src, ReductionLoop):
+        rl = src
+        if len(rl.partials) != 1:
             return None
+        smm = rl.partial
+        if not (isinstance(smm, Compute) and smm.op == "softmax_matmul" and smm.axis == rl.axis):
+            return None
+    elif isinstance(src, Compute) and src.op == "softmax_matmul":
+        smm = src
+    else:
+        return None
+    x, vload = smm.inputs
+    if not isinstance(vload, Load):
+        return None
+
+    def walk(body):
+        for s in body:
+            yield s
+            if isinstance(s, ReductionLoop):
+                yield from walk(s.body)
+    every = list(walk(loop.body))
+    found = _flash_scores(x, {id(s) for s in every})
+    if found is None:
+        return None
+    causal, scale, qload, ktload, nodes = found
+    allowed = {id(st), id(smm), id(vload)} | {id(n) for n in nodes}
+    if rl is not None:
+        allowed.add(id(rl))
+    if any(id(s) not in allowed for s in every):
+        return None
+    jax = smm.axis
     T = program.tensors
     qs, kts, vs, os_ = T[qload.source], T[ktload.source], T[vload.source], T[loop.out]
     nb = len(qs) - 2
@@ -136,8 +182,10 @@ def _match_flash(loop: ParallelLoop, program: Program):
     if len(iv) != len(qs):
         return None
     bax, iax, dax = iv[:nb], iv[nb], iv[nb + 1]
-    jax = rl.axis
-    if qload.index != bax + [iax, dax] or ktload.index != bax + [dax, jax] or \
+    if any(n.op == "causal" and n.axis != jax for n in nodes if isinstance(n, Compute)):
+        return None
+    dred = _contraction_axis(nodes[-3]) if isinstance(nodes[-3], Compute) else None
+    if dred is None or qload.index != bax + [iax, dred] or ktload.index != bax + [dred, jax] or \
             vload.index != bax + [jax, dax] or st.index != bax + [iax, dax]:
         return None
     N, D = qs[-2], qs[-1]
@@ -147,10 +195,13 @@ def _match_flash(loop: ParallelLoop, program: Program):
     tile = loop.tile_shape
     if any(t != 1 for t in tile[:nb]):
         return None
-    BM, BN = tile[nb], rl.tile
+    if D not in (64, 128):
+        return None
+    BM = tile[nb]
+    BN = rl.tile if rl is not None else FLASH_DEFAULT_BN[D]
     if tile[nb + 1] < D:
         return None
-    if BM not in FLASH_BM or BN not in (32, 64, 128) or D not in (64, 128):
+    if BM not in FLASH_BM or BN not in (32, 64, 128):
         return None
     if D == 128 and BN > 64:
         return None

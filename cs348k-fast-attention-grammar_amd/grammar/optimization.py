@@ -442,7 +442,8 @@ def stage1_sweep(program: Program, ev: Evaluator, ladder: tuple | None = None, c
 # Stage 2: rewrites (reference :517-793)
 # ---------------------------------------------------------------------------
 DEFAULT_RULES = ("hoist", "sink", "subtile_reduction", "unwrap_reduction", "merge", "merge_reductions",
-                 "reorder", "sink_compute", "hoist_compute", "fuse_softmax", "split_softmax")
+                 "reorder", "sink_compute", "hoist_compute", "fuse_softmax", "split_softmax",
+                 "fuse_softmax_chain")
 REFERENCE_RULES = DEFAULT_RULES[:7]
 
 
@@ -508,6 +509,9 @@ _KINDS = {
     "hoist_compute": (R.can_hoist_compute, R.hoist_compute),
     "fuse_softmax": (R.can_fuse_softmax, R.fuse_softmax),
     "split_softmax": (R.can_split_softmax, R.split_softmax),
+    "fuse_softmax_chain": (R.can_fuse_softmax_chain, R.fuse_softmax_chain),
+    "fuse_attention": (lambda p, c: R.can_fuse_softmax_chain(p, c, True),
+                       lambda p, c: R.fuse_softmax_chain(p, c, True)),
 }
 
 
@@ -604,6 +608,12 @@ def enumerate_rewrites(program: Program, rules, max_risk: int = 0, reduction_til
         for a, b in zip(program.body, program.body[1:]):
             if R.can_fuse_softmax(program, a, b)[0]:
                 out.append(_mk("fuse_softmax", f"fuse_softmax({a.out},{b.out})", program, a, b))
+    if "fuse_softmax_chain" in rules:
+        for b in program.body[2:]:
+            if R.can_fuse_softmax_chain(program, b)[0]:
+                out.append(_mk("fuse_softmax_chain", f"fuse_softmax_chain({b.out})", program, b))
+            if R.can_fuse_softmax_chain(program, b, True)[0]:
+                out.append(_mk("fuse_attention", f"fuse_attention({b.out})", program, b))
     if "split_softmax" in rules:
         for s in all_stmts:
             if isinstance(s, Compute) and s.op == "softmax_matmul" and R.can_split_softmax(program, s)[0]:

@@ -177,3 +177,25 @@ def test_gemm_lowered_batched_with_shared_weight():
     ref = np.maximum(0.5 * (a.double().numpy() @ w.double().numpy()), 0.0)
     mx, mn = O.errors(c.float().cpu().numpy(), ref)
     assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL
+
+
+@pytest.mark.parametrize("dt,causal", [("fp16", False), ("bf16", True)])
+def test_fuse_attention_from_atomic_program_runs_flash(dt, causal):
+    """The atomic 8/9-stage attention, fused by fuse_attention into one stage
+    (scores over the full key range, no key loop), renders to the flash
+    kernel and matches the fp32 oracle."""
+    dev = _cuda()
+    from grammar.hip_module import load_module
+    from grammar.workloads import AttnConfig, attention_inputs
+    import run_attention_search as RS
+    p = RS.build_attention(512, 64, tile=128, B=2, H=2, dtype=dt, causal=causal)
+    q = R.fuse_softmax_chain(p, p.body[-1], with_scores=True)
+    mod = load_module(emit_module(q))
+    assert [s["lowering"] for s in mod.plan["steps"]] == ["flash"]
+    qq, kt, v = attention_inputs(AttnConfig("t", 2, 2, 512, 64, dt, causal), seed=6, k_transposed=True)
+    o = mod.fn(kt.to(dev), qq.to(dev), v.to(dev))
+    torch.cuda.synchronize()
+    ref = O.attention(qq.float().numpy(), kt.float().numpy(), v.float().numpy(), causal=causal, k_transposed=True)
+    mx, mn = O.errors(o.float().cpu().numpy(), ref)
+    print(f"[fuse_attention] {dt} causal={causal}: max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)
+    assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL
