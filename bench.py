@@ -1,20 +1,32 @@
 #!/usr/bin/env python3
-"""Benchmark: attention forward TFLOP/s and % of the fp16 MFMA peak on one
-MI355X at B=4, H=16, N=1024, d=64.
+"""Benchmark: the best descent-found attention kernel's TFLOP/s and % of the
+fp16 MFMA peak on one MI355X at B=4, H=16, N=1024, d=64 (BASELINE.json
+config C2), with the descent's evals/min measured in the same run.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2|C3]
+                    [--search-seconds S] [--kernel descent|handwritten]
 
-A "step" is one attention forward over the whole batch, inputs resident in
-HBM. W untimed warmup steps, then exactly K steps between two hipEvents
-recorded on the stream the kernel runs on, after a device synchronize on both
-sides. Prints ONE JSON line on stdout (diagnostics go to stderr), with the
-roofline of the kernel and the CPU baseline (the staged naive attention in
-fp32 torch on this host's cores, on the same seeded inputs) beside it.
+1. Descent: the stochastic rewrite descent runs from the naive 8-stage
+   attention program (every stage its own kernel, full-extent tiles) for at
+   most S seconds; every variant is rendered to HIP, compiled with hiprtc,
+   checked against the fp32 closed form and timed. evals/min = timed variants
+   per wall minute. With S = 0 the committed best program of an earlier
+   descent (runs/attn_c2_best.json) is used instead.
+2. Timing: a "step" is one forward of the descent's best program over the
+   whole batch, inputs resident in HBM. W untimed warmup steps, then exactly
+   K steps between two hipEvents recorded on the stream the kernels run on,
+   after a device synchronize on both sides.
+3. Beside it: the hand-written gr_attn_fwd at its default tile, the C4 MLP
+   block through the two-GEMM gr_mlp_fwd, and the CPU baseline (the staged
+   naive attention in fp32 torch on this host's cores, same seeded inputs).
+
+Prints ONE JSON line on stdout; diagnostics go to stderr.
 """
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -27,7 +39,7 @@ sys.path.insert(0, REPO)
 
 METRIC = "attn fwd TFLOP/s, % fp16 MFMA peak (B4 H16 N1024 d64); descent evals/min"
 PEAK_TFLOPS = {"fp16": 2500.0, "bf16": 2500.0}     # MI355X dense MFMA, published
-HBM_PEAK_GBS = 8000.0
+BEST_PROGRAM = os.path.join(PKG, "runs", "attn_c2_best.json")
 
 
 def log(*a):
@@ -66,19 +78,55 @@ def cpu_baseline(cfg, seed: int, budget_s: float = 12.0) -> dict:
     }
 
 
-def measured_traffic(cfg, bm: int, bn: int):
-    """HBM bytes per launch for this kernel configuration from the committed
+def measured_traffic(key: str):
+    """HBM bytes per launch of the kernel named by `key` from the committed
     rocprofv3 FETCH_SIZE/WRITE_SIZE measurement (profiles/traffic.json),
     scaled by the copy-calibration factors; None if not measured."""
-    path = os.path.join(REPO, "profiles", "traffic.json")
     try:
-        with open(path) as f:
+        with open(os.path.join(REPO, "profiles", "traffic.json")) as f:
             t = json.load(f)
-        k = t["kernels"][f"{cfg.name}:{cfg.dtype}:bm{bm}:bn{bn}"]
+        k = t["kernels"][key]
         c = t["calibration"]
         return int((k["fetch_kib"] * c["fetch_factor"] + k["write_kib"] * c["write_factor"]) * 1024)
     except (OSError, KeyError, ValueError):
         return None
+
+
+def timed(step, steps: int, warmup: int) -> float:
+    """ms per step: warmup, then `steps` calls between two events on the
+    current stream, synchronized on both sides."""
+    import torch
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def run_descent(cfg, seconds: float, seed: int):
+    """The rewrite descent from the naive program for at most `seconds`."""
+    import run_attention_search as RS
+    from grammar.optimization import Evaluator, EvalConfig, SearchConfig, autotune
+    prog = RS.build_attention(cfg.N, cfg.D, B=cfg.B, H=cfg.H, dtype=cfg.dtype, causal=cfg.causal)
+    ev = Evaluator(EvalConfig(seed=seed), reference=RS.attention_reference(1.0 / math.sqrt(cfg.D), cfg.causal))
+    t0 = time.time()
+    best = autotune(prog, ev, SearchConfig(iters=500, N=4, K=5, seed=seed, verbose=False,
+                                            time_budget_s=seconds))
+    wall = time.time() - t0
+    st = ev.stats()
+    info = {"seconds": round(wall, 1), "timed_variants": st["timed_variants"],
+            "compiled_variants": st["compiled_variants"], "cache_hits": st["cache_hits"],
+            "evals_per_min": round(60.0 * st["timed_variants"] / max(wall, 1e-9), 1),
+            "best_loss_ms": round(ev(best), 6), "start": "naive 8-stage program, full-extent tiles",
+            "stages": [[l.out, list(l.tile_shape)] for l in best.body]}
+    return best, info
 
 
 def main() -> int:
@@ -88,16 +136,20 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="C2", choices=["C2", "C3"])
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--kernel", default="descent", choices=["descent", "handwritten"])
+    ap.add_argument("--search-seconds", type=float, default=60.0, dest="search_seconds",
+                    help="wall budget of the live descent (0 = use the committed best program)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--block-m", type=int, default=128, help="queries per workgroup")
-    ap.add_argument("--block-n", type=int, default=128, help="keys per tile")
+    ap.add_argument("--no-mlp", action="store_true")
+    ap.add_argument("--block-m", type=int, default=128, help="hand-written kernel: queries per workgroup")
+    ap.add_argument("--block-n", type=int, default=128, help="hand-written kernel: keys per tile")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run --steps plain device copies of MIB MiB "
                          "(the known-size reference that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one GPU only (the attention kernel on one GPU's share); "
+        print("bench.py: this build measures one GPU only (the kernels on one GPU's share of the heads); "
               "--gpus must be 1", file=sys.stderr)
         return 2
 
@@ -105,6 +157,9 @@ def main() -> int:
     from grammar.attention import flash_attention_fwd
     from grammar.workloads import CONFIGS, attention_inputs
 
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
     dev = torch.device("cuda:0")
     if args.copy_calibration:
         n = args.copy_calibration * (1 << 20) // 4
@@ -117,32 +172,84 @@ def main() -> int:
         return 0
 
     cfg = CONFIGS[args.config]
-    if cfg.D == 128 and args.block_n > 64:
-        args.block_n = 64
-    q, k, v = (t.to(dev) for t in attention_inputs(cfg, seed=args.seed))
-    out = torch.empty_like(q)
-    kernel = {"name": "gr_flash_fwd (hand-written)", "block_m": args.block_m, "block_n": args.block_n}
-
-    def step():
-        flash_attention_fwd(q, k, v, causal=cfg.causal, out=out,
-                            block_m=kernel["block_m"], block_n=kernel["block_n"])
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(args.steps):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / args.steps
-    tflops = cfg.flops / (ms * 1e-3) / 1e12
     peak = PEAK_TFLOPS[cfg.dtype]
-    log(f"[bench] {cfg.name}: {ms * 1e3:.2f} us/step  {tflops:.1f} TFLOP/s  {100 * tflops / peak:.1f}% of peak")
+    q, k, v = (t.to(dev) for t in attention_inputs(cfg, seed=args.seed))
+    kt = k.transpose(-1, -2).contiguous()
+
+    # 1. descent
+    search = None
+    if args.kernel == "descent":
+        from grammar.kernel_ast import emit_module, program_from_key
+        from grammar.hip_module import HipModule
+        if args.search_seconds > 0:
+            log(f"[bench] descent from the naive program, {args.search_seconds:.0f} s budget")
+            best, search = run_descent(cfg, args.search_seconds, args.seed)
+            log(f"[bench] descent: {search}")
+        else:
+            with open(BEST_PROGRAM) as f:
+                saved = json.load(f)
+            best = program_from_key(saved["key"])
+            search = {"source": os.path.relpath(BEST_PROGRAM, REPO), "evals_per_min": saved.get("evals_per_min")}
+        mod = HipModule(emit_module(best))
+        tensors = {"Q": q, "KT": kt, "V": v}
+        tensors.update(mod.allocate(dev))
+        plan = mod.bind(tensors)
+        main_k = mod.plan["steps"][-1]
+        kernel = {"name": main_k["kernel"], "source": "descent-found program rendered by the HIP backend",
+                  "lowering": [s["lowering"] for s in mod.plan["steps"]],
+                  "tiles": main_k.get("tiles"), "stages": len(mod.plan["steps"])}
+
+        def step():
+            plan.run()
+        out_t = tensors[mod.plan["outputs"][0]]
+        traffic_key = (f"{cfg.name}:{cfg.dtype}:{main_k['lowering']}:"
+                       f"bm{(main_k.get('tiles') or {}).get('block_m')}:bn{(main_k.get('tiles') or {}).get('block_n')}")
+    else:
+        out_t = torch.empty_like(q)
+        kernel = {"name": "gr_flash_fwd (hand-written)", "block_m": args.block_m, "block_n": args.block_n}
+
+        def step():
+            flash_attention_fwd(q, k, v, causal=cfg.causal, out=out_t, block_m=args.block_m, block_n=args.block_n)
+        traffic_key = f"{cfg.name}:{cfg.dtype}:flash:bm{args.block_m}:bn{args.block_n}"
+
+    # 2. the timed region
+    ms = timed(step, args.steps, args.warmup)
+    tflops = cfg.flops / (ms * 1e-3) / 1e12
+    log(f"[bench] {cfg.name} {kernel['name']}: {ms * 1e3:.2f} us/step  {tflops:.1f} TFLOP/s  "
+        f"{100 * tflops / peak:.1f}% of peak")
+    # tolerance check of the measured kernel's output against the fp32 closed form
+    s = torch.matmul(q.float(), kt.float()) / math.sqrt(cfg.D)
+    if cfg.causal:
+        n = cfg.N
+        s = s.masked_fill(torch.ones(n, n, dtype=torch.bool, device=dev).triu(1), float("-inf"))
+    ref = torch.matmul(torch.softmax(s, dim=-1), v.float())
+    d = (out_t.float() - ref).abs()
+    check = {"max_abs": float(d.max()), "mean_abs": float(d.mean()), "tol": [2e-2, 2e-3]}
+    check["pass"] = check["max_abs"] <= 2e-2 and check["mean_abs"] <= 2e-3
+    del s, ref, d
+
+    # 3. side measurements
+    hand = None
+    if args.kernel == "descent":
+        o2 = torch.empty_like(q)
+        hms = timed(lambda: flash_attention_fwd(q, k, v, causal=cfg.causal, out=o2, block_m=args.block_m,
+                                                block_n=args.block_n), args.steps, args.warmup)
+        hand = {"block_m": args.block_m, "block_n": args.block_n, "ms_per_step": round(hms, 6),
+                "tflops": round(cfg.flops / (hms * 1e-3) / 1e12, 3)}
+        log(f"[bench] hand-written gr_attn_fwd: {hms * 1e3:.2f} us/step  {hand['tflops']:.1f} TFLOP/s")
+    mlp = None
+    if not args.no_mlp:
+        from grammar.gemm import mlp_fwd
+        from grammar.workloads import C4, mlp_inputs
+        x, w1, w2 = (t.to(dev) for t in mlp_inputs(C4, seed=args.seed))
+        hbuf = torch.empty((C4.M, C4.Hd), dtype=x.dtype, device=dev)
+        y = torch.empty((C4.M, C4.Dm), dtype=x.dtype, device=dev)
+        mms = timed(lambda: mlp_fwd(x, w1, w2, h=hbuf, out=y), max(5, args.steps // 20), 3)
+        mlp = {"workload": "C4 MLP X[8192,4096] W1[4096,11008] SiLU W2[11008,4096] fp16, gr_mlp_fwd",
+               "ms_per_step": round(mms, 4), "tflops": round(C4.flops / (mms * 1e-3) / 1e12, 2),
+               "frac_of_peak": round(C4.flops / (mms * 1e-3) / 1e12 / PEAK_TFLOPS["fp16"], 4)}
+        log(f"[bench] C4 MLP: {mms:.3f} ms  {mlp['tflops']:.1f} TFLOP/s")
+        del x, w1, w2, hbuf, y
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -168,10 +275,13 @@ def main() -> int:
                    "B": cfg.B, "H": cfg.H, "N": cfg.N, "D": cfg.D, "causal": cfg.causal,
                    "kernel": kernel, "parallelism": "single GPU"},
         "pct_peak": round(100 * tflops / peak, 2),
-        "evals_per_min": None,
+        "evals_per_min": (search or {}).get("evals_per_min"),
+        "descent": search,
+        "check": check,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(tflops / peak, 5),
-                     "traffic": measured_traffic(cfg, args.block_m, args.block_n)},
+                     "frac": round(tflops / peak, 5), "traffic": measured_traffic(traffic_key)},
+        "handwritten": hand,
+        "mlp_c4": mlp,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)
