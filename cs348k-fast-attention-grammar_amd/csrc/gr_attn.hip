@@ -32,13 +32,16 @@ int dispatch_tiles(const gr_attn_args& a, int bm, int bn, hipStream_t st) {
   if (bm == 128 && bn == 64) return launch_flash<T, D, 64, 4, 1, CAUSAL, KT>(a, st);
   if (bm == 128 && bn == 32) return launch_flash<T, D, 32, 4, 1, CAUSAL, KT>(a, st);
   if (bm == 64 && bn == 64) return launch_flash<T, D, 64, 2, 1, CAUSAL, KT>(a, st);
-  // block_m = 129 / 257 select the software-pipelined schedule (tuning probe).
+  // block_m = 129 / 257 select the software-pipelined schedule (128 / 256 queries).
   if (bm == 129 && bn == 64) return launch_flash<T, D, 64, 4, 1, CAUSAL, KT, true>(a, st);
   if (bm == 129 && bn == 32) return launch_flash<T, D, 32, 4, 1, CAUSAL, KT, true>(a, st);
   if constexpr (D == 64) {
     if (bm == 128 && bn == 128) return launch_flash<T, D, 128, 4, 1, CAUSAL, KT>(a, st);
     if (bm == 256 && bn == 64) return launch_flash<T, D, 64, 4, 2, CAUSAL, KT>(a, st);
     if (bm == 256 && bn == 32) return launch_flash<T, D, 32, 4, 2, CAUSAL, KT>(a, st);
+    if (bm == 129 && bn == 128) return launch_flash<T, D, 128, 4, 1, CAUSAL, KT, true>(a, st);
+    if (bm == 257 && bn == 64) return launch_flash<T, D, 64, 4, 2, CAUSAL, KT, true>(a, st);
+    if (bm == 257 && bn == 32) return launch_flash<T, D, 32, 4, 2, CAUSAL, KT, true>(a, st);
   }
   return gr::fail(GR_E_ARG, "gr_attn_fwd: unsupported tile (block_m=%d, block_n=%d) for D=%d", bm, bn, D);
 }

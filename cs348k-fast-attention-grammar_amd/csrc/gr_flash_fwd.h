@@ -40,6 +40,12 @@ struct gr_attn_args {
   float scale_log2;             // softmax scale * log2(e)
 };
 
+// The online softmax moves its exponent base only when a row's max grows by
+// more than this many powers of two (p then stays <= 2^8, exact in fp16/bf16).
+#ifndef GR_RESCALE_LOG2
+#define GR_RESCALE_LOG2 8.0f
+#endif
+
 template <int V> struct gr_ic { static constexpr int value = V; };
 template <bool C, class X, class Y> struct gr_cond { typedef X type; };
 template <class X, class Y> struct gr_cond<false, X, Y> { typedef Y type; };
@@ -299,8 +305,11 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
             }
           }
       }
-      // Running max; the accumulators are rescaled only when some lane's max
-      // grew (otherwise the factor is exactly 1 and the multiply is skipped).
+      // Running reference max m. The exponent base is only moved (and the
+      // accumulators rescaled) when some lane's true max exceeds m by more
+      // than 2^GR_RESCALE_LOG2 in p; otherwise p = 2^((s - m) c) may reach
+      // that bound, which fp16/bf16 P, the fp32 row sum and fp32 O absorb
+      // exactly as well: O = sum p v / sum p does not depend on the base.
       float nmc[QB];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
@@ -311,18 +320,20 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
           for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][qb][r]);
         mt = fmaxf(mt, gr_xor32(mt));
         const float mn = fmaxf(m[qb], mt);
-        if (gr_any(mn > m[qb])) {
+        if (gr_any(mn > m[qb] + GR_RESCALE_LOG2 / c)) {    // m = -inf: any finite score moves it
           const float alpha = gr_exp2((m[qb] - mn) * c);   // m = -inf -> 0
           l[qb] *= alpha;
 #pragma unroll
           for (int db = 0; db < DB; ++db) o[db][qb] *= alpha;
+          m[qb] = mn;
         }
-        m[qb] = mn;
-        nmc[qb] = -((mn == -GR_INF) ? 0.f : mn) * c;
+        nmc[qb] = -((m[qb] == -GR_INF) ? 0.f : m[qb]) * c;
       }
-      if constexpr (PIPE) {
-        if (t + 1 < ntile && wave_active(t + 1)) gr_flash_qk<T, D, BN, QB>(sn, ks0 + (ODD ^ 1) * L::KS, qf, l32, g);
-      }
+      // PIPE: the next tile's scores, issued unconditionally so they share one
+      // basic block with this tile's softmax and P*V and can be interleaved
+      // with them (after the last tile this reads a stale but valid K slot and
+      // the result is dropped).
+      if constexpr (PIPE) gr_flash_qk<T, D, BN, QB>(sn, ks0 + (ODD ^ 1) * L::KS, qf, l32, g);
       const char* vt = vt0 + ODD * L::VT;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
@@ -350,6 +361,22 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
             for (int qb = 0; qb < QB; ++qb) o[db][qb] = MF::mma32(vf, pf[qb], o[db][qb]);
           }
         }
+      if constexpr (PIPE) {
+        // Interleave: per 32-key half block, the next tile's K reads and score
+        // MFMAs between this tile's exponentials and its P*V MFMAs, so the
+        // matrix cores run while the VALU works on the softmax.
+        constexpr int NQK = KB * DS * QB;          // next-tile score MFMAs
+        constexpr int NPV = KB * 2 * DB * QB;      // this tile's P*V MFMAs
+        constexpr int GROUPS = KB * 2;
+#pragma unroll
+        for (int i = 0; i < GROUPS; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x100, NQK / GROUPS, 0);   // K fragment reads
+          __builtin_amdgcn_sched_group_barrier(0x008, NQK / GROUPS, 0);   // score MFMAs (t+1)
+          __builtin_amdgcn_sched_group_barrier(0x002, 12 * QB, 0);        // softmax VALU
+          __builtin_amdgcn_sched_group_barrier(0x100, DB, 0);             // V^T fragment reads
+          __builtin_amdgcn_sched_group_barrier(0x008, NPV / GROUPS, 0);   // P*V MFMAs (t)
+        }
+      }
     }
     if (pf_k) kl.sstore(ks0 + (PIPE ? ODD : (ODD ^ 1)) * L::KS, tid);
     if (pf_v) vl.sstore(vt0 + (ODD ^ 1) * L::VT, tid);

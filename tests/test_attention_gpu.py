@@ -65,6 +65,14 @@ SMALL = [
     (1, 2, 512, 64, "bf16", False, True, 256, 32),
     (1, 2, 512, 128, "bf16", True, True, 128, 32),
     (1, 1, 128, 64, "fp16", True, False, 128, 64),
+    # block_m 129 / 257: the software-pipelined schedule (next tile's scores
+    # interleaved with this tile's softmax), 128 / 256 queries per workgroup
+    (1, 2, 512, 64, "fp16", False, True, 129, 64),
+    (1, 2, 512, 64, "bf16", True, False, 129, 128),
+    (1, 2, 512, 64, "fp16", True, True, 257, 64),
+    (1, 2, 512, 64, "bf16", False, False, 257, 32),
+    (1, 2, 512, 128, "fp16", True, True, 129, 32),
+    (1, 1, 128, 64, "fp16", False, False, 129, 128),
 ]
 
 
