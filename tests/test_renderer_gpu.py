@@ -199,3 +199,19 @@ def test_fuse_attention_from_atomic_program_runs_flash(dt, causal):
     mx, mn = O.errors(o.float().cpu().numpy(), ref)
     print(f"[fuse_attention] {dt} causal={causal}: max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)
     assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL
+
+
+@pytest.mark.parametrize("tile,sk", [(32, 32), (32, None), (16, 64)])
+def test_ln_mlp_block_on_gpu(tile, sk):
+    """The reference's MLP block (relu + residual + LayerNorm,
+    run_mlp_search.py:42-127) rendered to HIP (fp32, generic lowering) matches
+    the closed form (run_mlp_search.py:138-149) at the reference's tolerance."""
+    _cuda()
+    import run_mlp_search as RM
+    p = RM.build_mlp_ln(256, 256, 512, tile=tile, subtile_k=sk)
+    assert RM.verify(p, "ln")
+    ins = {k: v.cpu().numpy() for k, v in RM.mlp_inputs(256, 256, 512, "fp32", seed=3).items()}
+    got, mod = _gpu_run(p, ins)
+    want = run_program(p, ins)["out"]
+    print(f"[ln-block] tile={tile} sk={sk}: max|d| {float(np.max(np.abs(got - want))):.2e}", flush=True)
+    assert np.allclose(got, want, rtol=1e-3, atol=1e-3)
