@@ -114,3 +114,45 @@ __device__ __forceinline__ int gr_xcd_remap(int bid, int nblk) {
 
 // Wave-uniform "any lane" vote.
 __device__ __forceinline__ bool gr_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
+
+// ---------------------------------------------------------------------------
+// Row-lowering helpers: VEC consecutive elements of a row to/from fp32
+// registers with one vector access (the offset is a multiple of VEC), and
+// reductions across the 64 lanes of a wavefront.
+// ---------------------------------------------------------------------------
+template <int VEC, class T>
+__device__ __forceinline__ void gr_row_load(float (&d)[VEC], const T* p) {
+  if constexpr (VEC == 1) {
+    d[0] = (float)p[0];
+  } else {
+    typedef T vec_t __attribute__((ext_vector_type(VEC)));
+    const vec_t v = *reinterpret_cast<const vec_t*>(p);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) d[k] = (float)v[k];
+  }
+}
+
+template <int VEC, class T>
+__device__ __forceinline__ void gr_row_store(T* p, const float (&y)[VEC]) {
+  if constexpr (VEC == 1) {
+    p[0] = (T)y[0];
+  } else {
+    typedef T vec_t __attribute__((ext_vector_type(VEC)));
+    vec_t v;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) v[k] = (T)y[k];
+    *reinterpret_cast<vec_t*>(p) = v;
+  }
+}
+
+__device__ __forceinline__ float gr_wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+__device__ __forceinline__ float gr_wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}

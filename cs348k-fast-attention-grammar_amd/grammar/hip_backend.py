@@ -396,6 +396,271 @@ void {kname}({params}) {{
 
 
 # ---------------------------------------------------------------------------
+# Row lowering: pointwise stages and stages whose reductions run over the last
+# axis (row max / row sum, softmax pieces, LayerNorm). HBM-bound: one wave per
+# row, vectorised loads and stores, reductions by wave shuffles, nothing
+# staged in LDS.
+# ---------------------------------------------------------------------------
+ROW_WAVES = 4                 # waves (rows) per workgroup
+
+
+def _match_rows(loop: ParallelLoop, program: Program):
+    """Parameters of the row lowering if every value of `loop` is either an
+    element of a row (index = the loop's axes) or a per-row scalar (a row
+    reduction over the last axis, or a load of a [..., 1] tensor), else None."""
+    T = program.tensors
+    iv = list(loop.index_vars)
+    if len(iv) < 1:
+        return None
+    stores = [s for s in loop.body if isinstance(s, Store)]
+    if len(stores) != 1 or stores[0].dest != loop.out or stores[0].index != iv:
+        return None
+    st = stores[0]
+    out = tuple(T[loop.out])
+    nodes, reds = [], {}
+
+    def walk(body):
+        for x in body:
+            if isinstance(x, ReductionLoop):
+                if x.axis != iv[-1] or any(not (isinstance(c, Compute) and c.op in ROW_REDUCE_OPS and
+                                                c.axis == iv[-1]) for c in x.partials):
+                    return False
+                for c in x.partials:
+                    reds[id(c)] = c
+                if walk(x.body) is False:
+                    return False
+            elif isinstance(x, (Load, Compute)):
+                nodes.append(x)
+            elif not isinstance(x, Store):
+                return False
+        return True
+    if walk(loop.body) is False:
+        return None
+    C = None
+    for x in nodes:
+        if isinstance(x, Load):
+            if x.index != iv:
+                return None
+            sh = tuple(T[x.source])
+            if len(sh) != len(out) or any(a != b and a != 1 for a, b in zip(sh[:-1], out[:-1])):
+                return None
+            if sh[-1] != 1:
+                if C is not None and sh[-1] != C:
+                    return None
+                C = sh[-1]
+        elif x.op in ROW_REDUCE_OPS:
+            if x.axis != iv[-1]:
+                return None
+        elif x.op not in ELEMENTWISE_OPS:
+            return None
+        elif x.op == "causal" and (x.axis != iv[-1] or len(iv) < 2):
+            return None
+    if out[-1] != 1:
+        if C is not None and out[-1] != C:
+            return None
+        C = out[-1]
+    if C is None:
+        return None
+    kind = {}
+
+    def k(v):
+        """'e' (per element) or 's' (per row)."""
+        if id(v) in kind:
+            return kind[id(v)]
+        if isinstance(v, ReductionLoop):
+            r = "s"
+        elif isinstance(v, Load):
+            r = "e" if T[v.source][-1] != 1 else "s"
+        elif v.op in ROW_REDUCE_OPS:
+            if k(v.inputs[0]) != "e":
+                raise UnsupportedProgram("row reduction of a per-row value")
+            r = "s"
+        elif v.op == "causal":
+            r = "e"
+        else:
+            r = "e" if any(k(i) == "e" for i in v.inputs) else "s"
+        kind[id(v)] = r
+        return r
+    try:
+        ko = k(st.src)
+    except (UnsupportedProgram, AttributeError):
+        return None
+    if (ko == "e") != (out[-1] != 1):
+        return None
+    rows = _prod(out[:-1])
+    vec = 8 if C % 8 == 0 and C >= 512 else (4 if C % 4 == 0 and C >= 256 else 1)
+    return {"C": C, "rows": rows, "vec": vec, "out": out, "store": st}
+
+
+class _RowGen:
+    def __init__(self, loop, program, f):
+        self.loop, self.p, self.f = loop, program, f
+        self.T = CTYPE[program.dtype]
+        self.lines = []
+        self.n = 0
+        self.scal = {}          # id(value) -> C name of a computed per-row scalar
+        self.groups = {}        # id(partial) -> all partials of its multi-partial ReductionLoop
+
+        def walk(body):
+            for x in body:
+                if isinstance(x, ReductionLoop):
+                    if len(x.partials) > 1:
+                        for c in x.partials:
+                            self.groups[id(c)] = list(x.partials)
+                    walk(x.body)
+        walk(loop.body)
+
+    def fresh(self, p):
+        self.n += 1
+        return f"{p}{self.n}"
+
+    def kind(self, v):
+        if isinstance(v, ReductionLoop):
+            return "s"
+        if isinstance(v, Load):
+            return "e" if self.p.tensors[v.source][-1] != 1 else "s"
+        if v.op in ROW_REDUCE_OPS:
+            return "s"
+        if v.op == "causal":
+            return "e"
+        return "e" if any(self.kind(i) == "e" for i in v.inputs) else "s"
+
+    def red_of(self, v):
+        """(compute, op) if v is a row reduction value."""
+        if isinstance(v, ReductionLoop):
+            return v.partial
+        if isinstance(v, Compute) and v.op in ROW_REDUCE_OPS:
+            return v
+        return None
+
+    def row_off(self, name):
+        """C expression: element offset of this row's start in tensor `name`
+        (broadcast dims contribute nothing)."""
+        sh = self.p.tensors[name]
+        out = self.f["out"]
+        st = _row_major(sh)
+        terms = []
+        rem = "row"
+        # decompose the row index over out[:-1] (row-major)
+        ost = _row_major(out[:-1]) if len(out) > 1 else ()
+        for d in range(len(out) - 1):
+            if out[d] == 1 or sh[d] == 1:
+                continue
+            coord = f"((row / {ost[d]}LL) % {out[d]}LL)" if d > 0 else f"(row / {ost[d]}LL)"
+            terms.append(f"{coord} * {st[d]}LL")
+        return " + ".join(terms) if terms else "0LL"
+
+    def scalar(self, v, emit):
+        """Emit code computing per-row scalar v (all lanes hold it)."""
+        if id(v) in self.scal:
+            return self.scal[id(v)]
+        r = self.red_of(v)
+        if r is not None:
+            group = self.groups.get(id(r))
+            if group is not None:
+                # sibling partials of one ReductionLoop: one pass over the row
+                names = self.reduction(group, emit)
+                for c, nm in zip(group, names):
+                    self.scal[id(c)] = nm
+                return self.scal[id(r)]
+            name = self.reduction([r], emit)[0]
+        elif isinstance(v, Load):
+            name = self.fresh("s")
+            emit(f"const float {name} = (float)t_{v.source}[{self.row_off(v.source)}];")
+        else:
+            args = [self.scalar(i, emit) for i in v.inputs]
+            name = self.fresh("s")
+            emit(f"const float {name} = {_ew_expr(v.op, args, v.const)};")
+        self.scal[id(v)] = name
+        return name
+
+    def element_code(self, v, loads, pre, memo):
+        """C expression for element value v at column (c0 + k); loads collects
+        the element loads needed; scalars are emitted into `pre`."""
+        if id(v) in memo:
+            return memo[id(v)]
+        if self.kind(v) == "s":
+            e = self.scalar(v, pre)
+        elif isinstance(v, Load):
+            loads.setdefault(v.source, self.fresh("x"))
+            e = f"{loads[v.source]}[k]"
+        elif v.op == "causal":
+            a = self.element_code(v.inputs[0], loads, pre, memo)
+            R = self.f["out"][-2] if len(self.f["out"]) >= 2 else 1
+            e = f"((c0 + k) > (int)(row % {R}LL) ? -GR_INF : {a})"
+        else:
+            args = [self.element_code(i, loads, pre, memo) for i in v.inputs]
+            e = f"({_ew_expr(v.op, args, v.const)})"
+        memo[id(v)] = e
+        return e
+
+    def reduction(self, cs, emit):
+        """Row reductions `cs` computed in one pass over the row; returns the
+        names of their per-row results."""
+        vec, C = self.f["vec"], self.f["C"]
+        loads, memo, pre = {}, {}, []
+        exprs = [self.element_code(c.inputs[0], loads, pre.append, memo) for c in cs]
+        for x in pre:
+            emit(x)
+        accs = [self.fresh("r") for _ in cs]
+        for c, acc in zip(cs, accs):
+            emit(f"float {acc} = {'-GR_INF' if c.op == 'rowmax' else '0.f'};")
+        emit(f"for (int c0 = lane * {vec}; c0 < {C}; c0 += {64 * vec}) {{")
+        for src, nm in loads.items():
+            emit(f"  float {nm}[{vec}]; gr_row_load<{vec}>({nm}, t_{src} + {self.row_off(src)} + c0);")
+        emit(f"#pragma unroll")
+        emit(f"  for (int k = 0; k < {vec}; ++k) {{")
+        for c, acc, e in zip(cs, accs, exprs):
+            emit(f"    {acc} = fmaxf({acc}, {e});" if c.op == "rowmax" else f"    {acc} += {e};")
+        emit("  }")
+        emit("}")
+        for c, acc in zip(cs, accs):
+            emit(f"{acc} = {'gr_wave_max' if c.op == 'rowmax' else 'gr_wave_sum'}({acc});")
+        return accs
+
+    def render(self):
+        f = self.f
+        loop = self.loop
+        kname = f"{_cname(loop.out)}_kernel"
+        args = _loop_tensors(loop)
+        params = ", ".join(f"{'const ' if a != loop.out else ''}{self.T}* __restrict__ {_cname(a)}" for a in args)
+        body = []
+        emit = body.append
+        st = f["store"]
+        vec, C = f["vec"], f["C"]
+        if f["out"][-1] == 1:
+            val = self.scalar(st.src, emit)
+            emit(f"if (lane == 0) t_{loop.out}[{self.row_off(loop.out)}] = ({self.T}){val};")
+        else:
+            loads, memo, pre = {}, {}, []
+            expr = self.element_code(st.src, loads, pre.append, memo)
+            for x in pre:
+                emit(x)
+            emit(f"for (int c0 = lane * {vec}; c0 < {C}; c0 += {64 * vec}) {{")
+            for src, nm in loads.items():
+                emit(f"  float {nm}[{vec}]; gr_row_load<{vec}>({nm}, t_{src} + {self.row_off(src)} + c0);")
+            emit(f"  float y[{vec}];")
+            emit(f"#pragma unroll")
+            emit(f"  for (int k = 0; k < {vec}; ++k) y[k] = {expr};")
+            emit(f"  gr_row_store<{vec}>(t_{loop.out} + {self.row_off(loop.out)} + c0, y);")
+            emit("}")
+        ind = "\n  ".join(body)
+        code = f"""
+// stage {loop.out}: row lowering ({f['rows']} rows x {C}, one wave per row, {vec}-wide accesses)
+extern "C" __global__ __launch_bounds__({64 * ROW_WAVES})
+void {kname}({params}) {{
+  const int lane = threadIdx.x & 63;
+  const long long row = (long long)blockIdx.x * {ROW_WAVES} + (threadIdx.x >> 6);
+  if (row >= {f['rows']}LL) return;
+  {ind}
+}}
+"""
+        grid = _cdiv(f["rows"], ROW_WAVES)
+        return code, {"kernel": kname, "grid": [grid, 1, 1], "block": [64 * ROW_WAVES, 1, 1], "lds": 0,
+                      "args": args, "lowering": "rows", "tiles": {"vec": vec}}
+
+
+# ---------------------------------------------------------------------------
 # Generic lowering
 # ---------------------------------------------------------------------------
 class _View:
@@ -953,11 +1218,14 @@ def render_module(program: Program, fn_name: str = "fn") -> str:
     for loop in program.body:
         f = _match_flash(loop, program)
         gm = _match_gemm(loop, program) if f is None else None
+        rw = _match_rows(loop, program) if f is None and gm is None else None
         try:
             if f is not None:
                 code, step = _render_flash(loop, program, f)
             elif gm is not None:
                 code, step = _render_gemm(loop, program, gm)
+            elif rw is not None:
+                code, step = _RowGen(loop, program, rw).render()
             else:
                 code, step = _StageGen(loop, program, shapes).render()
         except LdsOverflow as e:

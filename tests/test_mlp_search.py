@@ -57,7 +57,7 @@ def test_ln_block_interpreter_matches_closed_form():
 def test_silu_fusion_lowers_both_stages_to_gemm():
     p = RM.build_mlp_silu(512, 256, 512, tile=128, subtile_k=64)
     steps = parse_plan(emit_module(p))["steps"]
-    assert [s["lowering"] for s in steps] == ["gemm", "generic", "gemm"]
+    assert [s["lowering"] for s in steps] == ["gemm", "rows", "gemm"]
     q = R.merge(p, p.body[0], p.body[1])
     steps = parse_plan(emit_module(q))["steps"]
     assert [s["lowering"] for s in steps] == ["gemm", "gemm"]

@@ -66,8 +66,11 @@ def test_unwrap_subtile_reproduces_source():
 def test_merge_reductions_single_load():
     from test_grammar import _two_reductions
     tr, a, b = _two_reductions()
-    assert emit_module(tr).count("(float)t_x[") == 2
-    assert emit_module(R.merge_reductions(tr, a, b)).count("(float)t_x[") == 1
+    def n_loads(src):
+        # generic lowering: scalar LDS fills; row lowering: one vector load per pass
+        return src.count("(float)t_x[") + src.count(", t_x + ")
+    assert n_loads(emit_module(tr)) == 2
+    assert n_loads(emit_module(R.merge_reductions(tr, a, b))) == 1
 
 
 def test_flash_lowering_selected_for_fp16_flash_structure():
@@ -85,9 +88,16 @@ def test_flash_lowering_selected_for_fp16_flash_structure():
 
 def test_lds_overflow_is_reported():
     from grammar.kernel_ast import Program, ParallelLoop, Store
-    x = Load("x", ["n", "m"])
-    r = Compute("relu", [x])
-    big = Program({"x": (512, 512), "o": (512, 512)},
-                  [ParallelLoop("o", (256, 512), ("n", "m"), [x, r, Store("o", r, ["n", "m"])])])
+    # an fp32 matmul stage (generic lowering) whose operand tiles need 1.5 MiB
+    x, w = Load("x", ["n", "k"]), Load("w", ["k", "m"])
+    r = Compute("matmul", [x, w])
+    big = Program({"x": (512, 512), "w": (512, 512), "o": (512, 512)},
+                  [ParallelLoop("o", (256, 512), ("n", "m"), [x, w, r, Store("o", r, ["n", "m"])])])
     with pytest.raises(LdsOverflow):
         render_module(big)
+    # a pointwise stage of the same tile needs no LDS: the row lowering streams it
+    y = Load("x", ["n", "m"])
+    rl = Compute("relu", [y])
+    pw = Program({"x": (512, 512), "o": (512, 512)},
+                 [ParallelLoop("o", (256, 512), ("n", "m"), [y, rl, Store("o", rl, ["n", "m"])])])
+    assert parse_plan(render_module(pw))["steps"][0]["lowering"] == "rows"

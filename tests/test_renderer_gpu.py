@@ -215,3 +215,38 @@ def test_ln_mlp_block_on_gpu(tile, sk):
     want = run_program(p, ins)["out"]
     print(f"[ln-block] tile={tile} sk={sk}: max|d| {float(np.max(np.abs(got - want))):.2e}", flush=True)
     assert np.allclose(got, want, rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("dt,causal,merges", [("fp16", False, 0), ("bf16", True, 0), ("fp16", False, 3)])
+def test_row_lowered_softmax_stages(dt, causal, merges):
+    """The softmax stages of the atomic attention program (scale, causal
+    mask, row max, subtract/exp, row sum, divide) lower to one-wave-per-row
+    kernels; after merges that gather them, the fused row stage computes
+    exp(x - rowmax x) / rowsum(...) in passes over the row. Output against the
+    fp32 oracle."""
+    dev = _cuda()
+    from grammar.hip_module import load_module
+    from grammar.workloads import AttnConfig, attention_inputs
+    import run_attention_search as RS
+    p = RS.build_attention(512, 64, tile=64, B=2, H=2, dtype=dt, causal=causal)
+    for l in p.body[1:-1]:
+        l.tile_shape = (1, 1, 64, 512)        # full rows, so merged stages keep one tile per value
+    for _ in range(merges):
+        names = [l.out for l in p.body]
+        i = names.index("sm") if "sm" in names else names.index("P") - 1
+        a = p.body[i]
+        b = p.body[i + 1]
+        if not R.can_merge(p, a, b)[0]:
+            break
+        p = R.merge(p, a, b)
+    mod = load_module(emit_module(p))
+    low = [s["lowering"] for s in mod.plan["steps"]]
+    print(f"[rows] {dt} causal={causal} merges={merges}: {[l.out for l in p.body]} {low}", flush=True)
+    assert low[0] == "gemm" and low[-1] == "gemm" and all(x == "rows" for x in low[1:-1])
+    q, kt, v = attention_inputs(AttnConfig("t", 2, 2, 512, 64, dt, causal), seed=8, k_transposed=True)
+    o = mod.fn(kt.to(dev), q.to(dev), v.to(dev))
+    torch.cuda.synchronize()
+    ref = O.attention(q.float().numpy(), kt.float().numpy(), v.float().numpy(), causal=causal, k_transposed=True)
+    mx, mn = O.errors(o.float().cpu().numpy(), ref)
+    print(f"[rows] max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)
+    assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL
