@@ -62,7 +62,8 @@ struct gr_gemm_cfg {
   static constexpr int A_BYTES = BM * BK * 2;
   static constexpr int B_BYTES = BN * BK * 2;
   static constexpr int STAGE = A_BYTES + B_BYTES;
-  static constexpr int LDS = 2 * STAGE;
+  static constexpr int C_BYTES = BM * BN * 2;     // the output tile, staged for coalesced stores
+  static constexpr int LDS = 2 * STAGE > C_BYTES ? 2 * STAGE : C_BYTES;
   static_assert(WM % 32 == 0 && WN % 32 == 0, "each wave owns whole 32x32 blocks");
   static_assert(BK % 16 == 0 && BK >= 16, "k tile");
   // 16-byte operand reads use chunk pairs (2*ks + lane/32): a row needs >= 2 chunks
@@ -152,22 +153,37 @@ __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
   }
 
   // epilogue: lane (l32, g) of block (i, j) holds row m = wm*WM + 32j + l32 and
-  // columns n = wn*WN + 32i + 8q + 4g + (0..3) in registers 4q..4q+3
+  // columns n = wn*WN + 32i + 8q + 4g + (0..3) in registers 4q..4q+3. The tile
+  // goes through LDS (16-byte chunks XOR-swizzled by row, as the operand
+  // tiles) so that the global stores are whole 16-byte chunks of contiguous
+  // row segments. The main loop's final barrier has retired every operand read.
+  constexpr int OCPR = BN / 8;
 #pragma unroll
   for (int j = 0; j < TM; ++j) {
-    T* crow = C + (long long)(wm * G::WM + j * 32 + l32) * a.c_sm;
+    const int row = wm * G::WM + j * 32 + l32;
 #pragma unroll
     for (int i = 0; i < TN; ++i)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n0 = wn * G::WN + i * 32 + 8 * q + 4 * g;
+        const int chunk = (wn * G::WN + i * 32 + 8 * q) >> 3;
         gr_u32x2 w;
         w[0] = gr_pack2<T>((T)gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + 0]),
                            (T)gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + 1]));
         w[1] = gr_pack2<T>((T)gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + 2]),
                            (T)gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + 3]));
-        *reinterpret_cast<gr_u32x2*>(crow + n0) = w;
+        *reinterpret_cast<gr_u32x2*>(lds + row * (BN * 2) + gr_swz<OCPR>(row, chunk) * 16 + g * 8) = w;
       }
+  }
+  __syncthreads();
+  constexpr int CHUNKS = BM * OCPR;
+#pragma unroll
+  for (int it = 0; it < (CHUNKS + NT - 1) / NT; ++it) {
+    const int cidx = tid + it * NT;
+    if (CHUNKS % NT == 0 || cidx < CHUNKS) {
+      const int row = cidx / OCPR, cc = cidx % OCPR;
+      const gr_u32x4 v = gr_ld16(lds + row * (BN * 2) + gr_swz<OCPR>(row, cc) * 16);
+      gr_st16(C + (long long)row * a.c_sm + cc * 8, v);
+    }
   }
 }
 

@@ -255,6 +255,12 @@ GEMM_WAVES_M = {32: 1, 64: 1, 128: 2, 256: 2}
 GEMM_WAVES_N = {32: 1, 64: 1, 128: 2, 256: 2}
 
 
+def _gemm_lds(bm, bn, bk):
+    """LDS bytes of the GEMM kernel: two operand stages, or the staged output
+    tile (gr_gemm_cfg::LDS)."""
+    return max(2 * (bm + bn) * bk * 2, bm * bn * 2)
+
+
 def _gemm_waves(bm, bn):
     wgm, wgn = GEMM_WAVES_M[bm], GEMM_WAVES_N[bn]
     if bm == 256 and bn == 256:
@@ -353,7 +359,7 @@ def _match_gemm(loop: ParallelLoop, program: Program):
         BK //= 2
     if BK not in (16, 32, 64, 128) or K % BK:
         BK = 32 if K % 32 == 0 else (16 if K % 16 == 0 else 0)
-    if not BK or 2 * (BM + BN) * BK * 2 > LDS_LIMIT:
+    if not BK or _gemm_lds(BM, BN, BK) > LDS_LIMIT:
         return None
     if M * K % 8 or K * N % 8 or K % 8 or N % 8:
         return None
@@ -389,7 +395,7 @@ void {kname}({params}) {{
 }}
 """
     grid = (f["M"] // f["BM"]) * (f["N"] // f["BN"])
-    lds = 2 * (f["BM"] + f["BN"]) * f["BK"] * 2
+    lds = _gemm_lds(f["BM"], f["BN"], f["BK"])
     return code, {"kernel": kname, "grid": [grid, f["batch"], 1], "block": [nt, 1, 1], "lds": lds,
                   "args": args, "lowering": "gemm",
                   "tiles": {"block_m": f["BM"], "block_n": f["BN"], "block_k": f["BK"]}}
