@@ -273,6 +273,11 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
     kl.gload(Kp + k_tile, tid);
     kl.sstore(ks0 + L::KS, tid);
   }
+  // Retire every prologue load (the Q fragments in particular) before the
+  // loop: the compiler's wait-counter tracking cannot see through the loop
+  // back edge that they completed, and would otherwise wait on the vmcnt of
+  // the in-flight next-tile prefetch at the first score MFMA of every tile.
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   // Two score buffers used in turn (the loop is unrolled by two), so handing
   // the next tile's scores over costs no register moves.
