@@ -367,3 +367,21 @@ def test_sink_compute_rejects_loop_axis_reduction():
     rl = next(s for s in p2.body[0].body if isinstance(s, ReductionLoop))
     mx = next(s for s in p2.body[0].body if isinstance(s, Compute) and s.op == "rowmax")
     assert not R.can_sink_compute(p2, mx, rl)[0]
+
+
+def test_program_from_key_binds_duplicate_loads_by_tile():
+    """A stage that reads one tensor twice at different tile shapes (the row
+    max over the full row, the subtraction over the tile) rebuilds from its
+    structural key with each operand bound to the right load."""
+    import run_attention_search as RS
+    from grammar import rewrites as Rw
+    from grammar.kernel_ast import _infer_program, program_from_key
+    p = RS.build_attention(64, 16, tile=16)
+    names = [l.out for l in p.body]
+    i = names.index("mx")
+    q = Rw.merge(p, p.body[i], p.body[i + 1])
+    _infer_program(q)
+    k = structural_key(q)
+    r = program_from_key(k)
+    _infer_program(r)
+    assert structural_key(r) == k
