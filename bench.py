@@ -17,7 +17,8 @@ config C2), with the descent's evals/min measured in the same run.
    K steps between two hipEvents recorded on the stream the kernels run on,
    after a device synchronize on both sides.
 3. Beside it: the hand-written gr_attn_fwd at its default tile, the C4 MLP
-   block through the two-GEMM gr_mlp_fwd, and the CPU baseline (the staged
+   block through the two-GEMM gr_mlp_fwd, the committed descent-found programs
+   for C3 (causal attention) and C4 (MLP), and the CPU baseline (the staged
    naive attention in fp32 torch on this host's cores, same seeded inputs).
 
 Prints ONE JSON line on stdout; diagnostics go to stderr.
@@ -110,6 +111,59 @@ def timed(step, steps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) / steps
 
 
+def side_programs(steps: int, seed: int) -> dict:
+    """The committed descent-found programs for C3 (causal attention) and C4
+    (MLP block), rendered, timed and tolerance-checked on sampled outputs."""
+    import torch
+    from grammar.hip_module import HipModule
+    from grammar.kernel_ast import emit_module, program_from_key
+    from grammar.workloads import C3, C4, attention_inputs, mlp_inputs
+    dev = torch.device("cuda:0")
+    out = {}
+    for name, cfg in (("C3", C3), ("C4", C4)):
+        path = os.path.join(PKG, "runs", f"{'attn_c3' if name == 'C3' else 'mlp_c4'}_best.json")
+        try:
+            with open(path) as f:
+                saved = json.load(f)
+        except OSError:
+            continue
+        mod = HipModule(emit_module(program_from_key(saved["key"])))
+        if name == "C3":
+            q, k, v = (t.to(dev) for t in attention_inputs(cfg, seed=seed))
+            tensors = {"Q": q, "KT": k.transpose(-1, -2).contiguous(), "V": v}
+        else:
+            x, w1, w2 = (t.to(dev) for t in mlp_inputs(cfg, seed=seed))
+            tensors = {"X": x, "W1": w1, "W2": w2}
+        tensors.update(mod.allocate(dev))
+        plan = mod.bind(tensors)
+        ms = timed(lambda: plan.run(), max(5, steps // 20), 3)
+        res = tensors[mod.plan["outputs"][0]].float()
+        if name == "C3":
+            errs = []
+            for b, h in ((0, 0), (1, 31)):
+                sc = torch.matmul(q[b, h].float(), k[b, h].float().t()) / math.sqrt(cfg.D)
+                sc = sc.masked_fill(torch.ones_like(sc, dtype=torch.bool).triu(1), float("-inf"))
+                errs.append((res[b, h] - torch.softmax(sc, -1) @ v[b, h].float()).abs())
+            d = torch.cat([e.reshape(-1) for e in errs])
+            sample = "heads (0,0) and (1,31) against fp32 softmax(QK^T/sqrt(d) + causal mask) V"
+        else:
+            rows = torch.randperm(cfg.M, generator=torch.Generator("cpu").manual_seed(1))[:256].to(dev)
+            ref = torch.nn.functional.silu(x[rows].float() @ w1.float()) @ w2.float()
+            d = (res[rows] - ref).abs()
+            sample = "256 sampled rows against fp32 SiLU(X W1) W2"
+        out[name] = {"source": os.path.relpath(path, REPO), "ms_per_step": round(ms, 5),
+                     "tflops": round(cfg.flops / (ms * 1e-3) / 1e12, 2),
+                     "frac_of_peak": round(cfg.flops / (ms * 1e-3) / 1e12 / PEAK_TFLOPS[cfg.dtype], 4),
+                     "lowering": [s["lowering"] for s in mod.plan["steps"]],
+                     "check": {"max_abs": float(d.max()), "mean_abs": float(d.mean()), "sample": sample,
+                               "pass": float(d.max()) <= 2e-2 and float(d.mean()) <= 2e-3}}
+        log(f"[bench] {name} descent-found program: {ms:.4f} ms  {out[name]['tflops']:.1f} TFLOP/s  "
+            f"check {out[name]['check']['pass']}")
+        del tensors, plan, mod
+        torch.cuda.empty_cache()
+    return out
+
+
 def run_descent(cfg, seconds: float, seed: int):
     """The rewrite descent from the naive program for at most `seconds`."""
     import run_attention_search as RS
@@ -141,6 +195,8 @@ def main() -> int:
                     help="wall budget of the live descent (0 = use the committed best program)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-mlp", action="store_true")
+    ap.add_argument("--no-side", action="store_true",
+                    help="skip the committed descent-found C3 / C4 programs")
     ap.add_argument("--block-m", type=int, default=128, help="hand-written kernel: queries per workgroup")
     ap.add_argument("--block-n", type=int, default=128, help="hand-written kernel: keys per tile")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -251,6 +307,8 @@ def main() -> int:
         log(f"[bench] C4 MLP: {mms:.3f} ms  {mlp['tflops']:.1f} TFLOP/s")
         del x, w1, w2, hbuf, y
 
+    side = None if args.no_side else side_programs(args.steps, args.seed)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(cfg, args.seed)
@@ -282,6 +340,7 @@ def main() -> int:
                      "frac": round(tflops / peak, 5), "traffic": measured_traffic(traffic_key)},
         "handwritten": hand,
         "mlp_c4": mlp,
+        "descent_programs": side,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

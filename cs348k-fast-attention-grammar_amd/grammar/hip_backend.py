@@ -1249,11 +1249,16 @@ def render_module(program: Program, fn_name: str = "fn") -> str:
 
 
 def flash_stage_indices(program: Program) -> set:
-    """Indices of the stages that lower to a hand-tiled MFMA kernel (flash or
-    GEMM): their working set lives in registers and a fixed LDS ring, not in
-    per-value LDS tiles."""
-    return {i for i, loop in enumerate(program.body)
-            if _match_flash(loop, program) is not None or _match_gemm(loop, program) is not None}
+    """Indices of the stages whose lowering does not stage per-value tiles in
+    LDS: the flash and GEMM kernels (registers and a fixed LDS ring) and the
+    row lowering (streams rows through registers)."""
+    out = set()
+    for i, loop in enumerate(program.body):
+        if _match_flash(loop, program) is not None or _match_gemm(loop, program) is not None:
+            out.add(i)
+        elif _match_rows(loop, program) is not None:
+            out.add(i)
+    return out
 
 
 def parse_plan(src: str) -> dict:

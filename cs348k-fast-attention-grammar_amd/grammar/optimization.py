@@ -160,17 +160,26 @@ class Evaluator:
                 "wall_s": el, "evals_per_min": 60.0 * self._runs / el}
 
     # ---- scoring -------------------------------------------------------------
+    def _tile_excess(self, program: Program) -> int:
+        """Bytes by which the stages staged tile by tile in LDS exceed the
+        per-stage tile budget (0 when within it, or when the gate is off)."""
+        if not self.cfg.mem_budget:
+            return 0
+        from .hip_backend import flash_stage_indices
+        try:
+            per = kernel_peak_tile_bytes(program)
+        except (AssertionError, ValueError, KeyError):
+            return 0
+        for i in flash_stage_indices(program):
+            per[i] = 0
+        return sum(max(0, k - self.cfg.mem_budget) for k in per)
+
     def _gated(self, program: Program):
         """Static penalty (memory / compile risk), or None if the program may be compiled."""
         cfg = self.cfg
-        if cfg.mem_budget:
-            from .hip_backend import flash_stage_indices
-            per = kernel_peak_tile_bytes(program)
-            for i in flash_stage_indices(program):
-                per[i] = 0
-            if per and max(per) > cfg.mem_budget:
-                excess = sum(max(0, k - cfg.mem_budget) for k in per)
-                return MEM_PENALTY_BASE + excess / 1024.0
+        excess = self._tile_excess(program)
+        if excess:
+            return MEM_PENALTY_BASE + excess / 1024.0
         if cfg.max_compile_risk:
             per = kernel_compile_risk(program)
             if per and max(per) > cfg.max_compile_risk:
@@ -189,7 +198,9 @@ class Evaluator:
         except LdsOverflow as e:
             if self.cfg.log:
                 print(f"{self._tag} {e} -> penalty", flush=True)
-            return MEM_PENALTY_BASE + e.need / 1024.0
+            # the LDS excess and the tile-budget excess of the other stages add
+            # up, so a program's penalty falls whichever stage shrinks
+            return MEM_PENALTY_BASE + (e.need + self._tile_excess(program)) / 1024.0
         except Exception as e:
             if self.cfg.log:
                 print(f"{self._tag} emit failed ({type(e).__name__}: {e}) -> inf", flush=True)

@@ -1,0 +1,44 @@
+"""bench.py contract checks that need no GPU: one GPU only, and the traffic
+table lookup."""
+import json
+import os
+import subprocess
+import sys
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_more_than_one_gpu_exits_with_message():
+    r = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_measured_traffic_uses_calibrated_counters():
+    sys.path.insert(0, REPO)
+    import bench
+    t = json.load(open(os.path.join(REPO, "profiles", "traffic.json")))
+    key = "C2:fp16:flash:bm128:bn64"
+    k, c = t["kernels"][key], t["calibration"]
+    want = int((k["fetch_kib"] * c["fetch_factor"] + k["write_kib"] * c["write_factor"]) * 1024)
+    assert bench.measured_traffic(key) == want
+    # close to the algorithmic 32 MiB of Q, K^T, V read and O written
+    assert abs(want - 4 * 4 * 16 * 1024 * 64 * 2) / want < 0.05
+    assert bench.measured_traffic("no:such:kernel") is None
+
+
+def test_committed_best_programs_rebuild():
+    sys.path.insert(0, os.path.join(REPO, "cs348k-fast-attention-grammar_amd"))
+    from grammar.kernel_ast import emit_module, program_from_key, structural_key
+    from grammar.hip_backend import parse_plan
+    runs = os.path.join(REPO, "cs348k-fast-attention-grammar_amd", "runs")
+    lowerings = {}
+    for name in ("attn_c2_best.json", "attn_c3_best.json", "mlp_c4_best.json"):
+        saved = json.load(open(os.path.join(runs, name)))
+        p = program_from_key(saved["key"])
+        assert structural_key(program_from_key(structural_key(p))) == structural_key(p)
+        lowerings[name] = [s["lowering"] for s in parse_plan(emit_module(p))["steps"]]
+    assert lowerings["attn_c2_best.json"] == ["flash"]
+    assert lowerings["attn_c3_best.json"] == ["flash"]
+    assert lowerings["mlp_c4_best.json"] == ["gemm", "gemm"]
