@@ -314,6 +314,10 @@ def main() -> int:
         cpu = cpu_baseline(cfg, args.seed)
         log(f"[bench] cpu baseline: {cpu['ms']:.1f} ms/rep  {cpu['value'] * 1e3:.2f} GFLOP/s on {cpu['cores']} threads")
         cpu.pop("ms")
+        c1 = cpu_baseline(CONFIGS["C1"], args.seed, budget_s=3.0)
+        log(f"[bench] cpu baseline C1: {c1['ms']:.2f} ms/rep  {c1['value'] * 1e3:.2f} GFLOP/s")
+        c1.pop("ms")
+        cpu["C1"] = c1
 
     rec = {
         "metric": METRIC,
