@@ -18,7 +18,7 @@ int launch_flash(const gr_attn_args& a, hipStream_t st) {
     return gr::fail(GR_E_ARG, "gr_attn_fwd: N=%d must be a multiple of block_m=%d and block_n=%d", a.N, BM, BN);
   const long long nblk = (long long)a.B * a.H * (a.N / BM);
   if (nblk <= 0 || nblk > 0x7fffffffLL) return gr::fail(GR_E_ARG, "gr_attn_fwd: grid size %lld out of range", nblk);
-  hipLaunchKernelGGL((gr_flash_fwd_kernel<T, D, BN, NW, QB, CAUSAL, KT, PIPE>), dim3((unsigned)nblk), dim3(NW * 64), LDS,
+  hipLaunchKernelGGL((gr_flash_fwd_kernel<T, D, BN, NW, QB, CAUSAL, KT, PIPE, true>), dim3((unsigned)nblk), dim3(NW * 64), LDS,
                      st, a);
   return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_fwd launch");
 }

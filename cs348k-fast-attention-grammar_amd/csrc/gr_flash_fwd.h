@@ -16,10 +16,14 @@
 //    makes the S^T accumulators of each half-wave hold 8 *consecutive* keys;
 //    those registers are then exactly the B operand of the P*V MFMA, and V^T
 //    can be read with one 16-byte LDS load per MFMA.
-//  * Q stays in registers for the whole kernel. K and V^T tiles are double
+//  * Q stays in registers for the whole kernel. K and V tiles are double
 //    buffered in LDS (one barrier per key tile) and prefetched from global
 //    into registers one tile ahead. 16-byte LDS chunks are XOR-swizzled by row
 //    so both the tile writes and the MFMA operand reads are bank-conflict free.
+//  * With TR (the default in every launch path) V, and K when it comes
+//    transposed (KT), are copied into LDS as laid out in memory and the MFMA
+//    fragments are read back with gfx950's transposing LDS read, so no tile is
+//    transposed in registers on its way in.
 //  * Causal: key tiles past the block's last query are never visited; waves
 //    whose queries all precede a tile skip its math; the mask is applied only
 //    on diagonal tiles. Heavy query tiles are scheduled first.
@@ -70,10 +74,23 @@ __device__ __forceinline__ int gr_swz(int row, int chunk) {
   else return chunk;
 }
 
+// Swizzle of tiles that are read back only through gr_tr_frag (transposing
+// reads): a fragment read touches 4 consecutive rows x 4 consecutive 16-byte
+// chunks per half-wave, and these XOR patterns put those 16 chunks on 16
+// distinct 4-bank groups for every row length; the 16-byte tile writes of a
+// row (or of two 128-byte rows) stay conflict free as well.
+template <int CPR>
+__device__ __forceinline__ int gr_swz_tr(int row, int chunk) {
+  if constexpr (CPR >= 16) return chunk ^ ((row & 3) << 2);
+  else if constexpr (CPR == 8) return chunk ^ (((row >> 1) & 1) << 2);
+  else return chunk;
+}
+
 // Global [ROWS][COLS] tile (row stride ld elements) -> LDS rows, same shape.
 // Per-thread global and LDS offsets are computed once (init) and reused for
-// every tile, so the main loop spends no VALU on address arithmetic.
-template <class T, int ROWS, int COLS, int NT, bool PERM>
+// every tile, so the main loop spends no VALU on address arithmetic. TRSWZ
+// selects the swizzle of tiles read through gr_tr_frag.
+template <class T, int ROWS, int COLS, int NT, bool PERM, bool TRSWZ = false>
 struct gr_row_loader {
   static constexpr int CPR = COLS / 8;
   static constexpr int CHUNKS = ROWS * CPR;
@@ -88,7 +105,7 @@ struct gr_row_loader {
       const int row = c / CPR, cc = c % CPR;
       const int prow = PERM ? gr_perm32(row) : row;
       goff[i] = (int)(row * ld) + cc * 8;
-      loff[i] = prow * (COLS * 2) + gr_swz<CPR>(prow, cc) * 16;
+      loff[i] = prow * (COLS * 2) + (TRSWZ ? gr_swz_tr<CPR>(prow, cc) : gr_swz<CPR>(prow, cc)) * 16;
     }
   }
   __device__ __forceinline__ bool live(int i, int tid) const { return CHUNKS % NT == 0 || tid + i * NT < CHUNKS; }
@@ -163,6 +180,35 @@ struct gr_tr_loader {
   }
 };
 
+// MFMA operand fragment (8 consecutive k for one m/n per lane, as the 16-byte
+// reads of k-contiguous tiles give) from an LDS tile laid out the other way:
+// [K rows][COLS] with the m/n index contiguous, swizzled by gr_swz_tr. Two
+// gfx950 transposing reads (ds_read_b64_tr_b16): within each 16-lane group,
+// lane 4a+b receives element b of the 4-element vectors addressed by lanes
+// a, a+4, a+8, a+12. Lane l addresses row k0 + 8(l/32) + 4h + (l/4)%4 and
+// column n0 + 16((l/16)%2) + 4c, so that it receives rows k0 + 8(l/32) +
+// 4h + 0..3 of column n0 + perm(l%32), where c = l%4 (PERM: its two bits
+// swapped, i.e. column bits 2 and 3 swapped, as gr_perm32 does to K rows).
+template <class T, int COLS, bool PERM>
+__device__ __forceinline__ typename gr_mfma<T>::vec8 gr_tr_frag(const char* tile, int k0, int n0, int lane) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
+  const int c = lane & 3;
+  const int cc = PERM ? (((c & 1) << 1) | (c >> 1)) : c;
+  const int col = n0 + 16 * ((lane >> 4) & 1) + 4 * cc;
+  gr_u32x4 r;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int row = k0 + 8 * (lane >> 5) + 4 * h + ((lane >> 2) & 3);
+    const char* p = tile + row * (COLS * 2) + gr_swz_tr<COLS / 8>(row, col >> 3) * 16 + (col & 7) * 2;
+    const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(__attribute__((address_space(3))) char*)(char*)p);
+    const gr_u32x2 w = __builtin_bit_cast(gr_u32x2, v);
+    r[2 * h] = w[0];
+    r[2 * h + 1] = w[1];
+  }
+  return gr_as<typename gr_mfma<T>::vec8>(r);
+}
+
 template <int D, int BN>
 struct gr_flash_lds {
   static constexpr int KS = BN * D * 2;
@@ -172,7 +218,7 @@ struct gr_flash_lds {
 
 // One key tile of S^T = K Q^T for this wave: s[kb][qb] (32 keys x 32 queries
 // per block). K rows sit in LDS with the row permutation gr_perm32.
-template <class T, int D, int BN, int QB>
+template <class T, int D, int BN, int QB, bool KTR = false>
 __device__ __forceinline__ void gr_flash_qk(gr_f32x16 (&s)[BN / 32][QB], const char* ks,
                                             const typename gr_mfma<T>::vec8 (&qf)[QB][D / 16], int l32, int g) {
   typedef typename gr_mfma<T>::vec8 vec8;
@@ -185,14 +231,16 @@ __device__ __forceinline__ void gr_flash_qk(gr_f32x16 (&s)[BN / 32][QB], const c
     const int row = kb * 32 + l32;
 #pragma unroll
     for (int ds = 0; ds < D / 16; ++ds) {
-      const vec8 af = gr_as<vec8>(gr_ld16(ks + row * (D * 2) + gr_swz<D / 8>(row, 2 * ds + g) * 16));
+      // KTR: K^T tile [D][BN] read transposed; else K rows [BN][D] (rows bit-permuted)
+      const vec8 af = KTR ? gr_tr_frag<T, BN, true>(ks, ds * 16, kb * 32, l32 + 32 * g)
+                          : gr_as<vec8>(gr_ld16(ks + row * (D * 2) + gr_swz<D / 8>(row, 2 * ds + g) * 16));
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) s[kb][qb] = gr_mfma<T>::mma32(af, qf[qb][ds], s[kb][qb]);
     }
   }
 }
 
-template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT, bool PIPE>
+template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT, bool PIPE, bool TR = false>
 __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* lds) {
   typedef gr_mfma<T> MF;
   typedef typename MF::vec8 vec8;
@@ -244,9 +292,12 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
   char* vt0 = lds + 2 * L::KS;
 
   // K tile source: natural rows [BN keys][D] or transposed [D][BN keys].
+  // TR: V and (KT layout) K^T tiles land in LDS as they are in memory and the
+  // MFMA fragments are read back transposed (gr_tr_frag).
+  constexpr bool KTR = TR && KT_LAYOUT;
   typedef gr_row_loader<T, BN, D, NT, true> KRows;
-  typedef gr_tr_loader<T, D, BN, NT, true> KCols;
-  typedef gr_tr_loader<T, BN, D, NT, false> VLoad;
+  typedef typename gr_cond<KTR, gr_row_loader<T, D, BN, NT, false, true>, gr_tr_loader<T, D, BN, NT, true>>::type KCols;
+  typedef typename gr_cond<TR, gr_row_loader<T, BN, D, NT, false, true>, gr_tr_loader<T, BN, D, NT, false>>::type VLoad;
   typename gr_cond<KT_LAYOUT, KCols, KRows>::type kl;
   VLoad vl;
   kl.init(tid, a.k_sn);
@@ -283,7 +334,7 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
   // the next tile's scores over costs no register moves.
   gr_f32x16 sA[KB][QB], sB[PIPE ? KB : 1][QB];
   if (PIPE) {
-    gr_flash_qk<T, D, BN, QB>(sA, ks0, qf, l32, g);
+    gr_flash_qk<T, D, BN, QB, KTR>(sA, ks0, qf, l32, g);
     __syncthreads();   // every wave is done with slot 0 of K before K_2 lands there
   }
 
@@ -296,7 +347,7 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
     if (pf_v) vl.gload(Vp + (t + 1) * v_tile, tid);
     const int k0 = t * BN;
     if (wave_active(t)) {
-      if constexpr (!PIPE) gr_flash_qk<T, D, BN, QB>(s, ks0 + ODD * L::KS, qf, l32, g);
+      if constexpr (!PIPE) gr_flash_qk<T, D, BN, QB, KTR>(s, ks0 + ODD * L::KS, qf, l32, g);
       if (CAUSAL && k0 + BN - 1 > qw) {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
@@ -338,7 +389,7 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
       // basic block with this tile's softmax and P*V and can be interleaved
       // with them (after the last tile this reads a stale but valid K slot and
       // the result is dropped).
-      if constexpr (PIPE) gr_flash_qk<T, D, BN, QB>(sn, ks0 + (ODD ^ 1) * L::KS, qf, l32, g);
+      if constexpr (PIPE) gr_flash_qk<T, D, BN, QB, KTR>(sn, ks0 + (ODD ^ 1) * L::KS, qf, l32, g);
       const char* vt = vt0 + ODD * L::VT;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
@@ -361,7 +412,8 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
 #pragma unroll
           for (int db = 0; db < DB; ++db) {
             const int row = db * 32 + l32;
-            const vec8 vf = gr_as<vec8>(gr_ld16(vt + row * (BN * 2) + gr_swz<BN / 8>(row, 4 * kb + 2 * hf + g) * 16));
+            const vec8 vf = TR ? gr_tr_frag<T, D, false>(vt, kb * 32 + 16 * hf, db * 32, l32 + 32 * g)
+                               : gr_as<vec8>(gr_ld16(vt + row * (BN * 2) + gr_swz<BN / 8>(row, 4 * kb + 2 * hf + g) * 16));
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) o[db][qb] = MF::mma32(vf, pf[qb], o[db][qb]);
           }
@@ -433,10 +485,10 @@ struct gr_flash_wpe {
 
 // Kernel wrapper used by the prebuilt library; the grammar renderer emits its
 // own wrappers with baked-in shapes around the same body.
-template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT, bool PIPE>
+template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT, bool PIPE, bool TR = false>
 __global__ __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(gr_flash_wpe<D, BN, NW, QB, KT_LAYOUT, PIPE>::value)))
 void gr_flash_fwd_kernel(gr_attn_args a) {
   extern __shared__ __attribute__((aligned(16))) char gr_lds[];
-  gr_flash_fwd_body<T, D, BN, NW, QB, CAUSAL, KT_LAYOUT, PIPE>(a, gr_lds);
+  gr_flash_fwd_body<T, D, BN, NW, QB, CAUSAL, KT_LAYOUT, PIPE, TR>(a, gr_lds);
 }

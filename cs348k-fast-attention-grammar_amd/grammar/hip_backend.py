@@ -237,7 +237,7 @@ void {kname}({params}) {{
   a.o_sb = {N * D}LL; a.o_sh = 0; a.o_sn = {D};
   a.B = {f['lead']}; a.H = 1; a.N = {N};
   a.scale_log2 = {_flt(f['scale'] * LOG2E)};
-  gr_flash_fwd_body<{T}, {D}, {f['BN']}, {f['NW']}, {f['QB']}, {'true' if f['causal'] else 'false'}, true, {pipe}>(a, gr_flash_smem);
+  gr_flash_fwd_body<{T}, {D}, {f['BN']}, {f['NW']}, {f['QB']}, {'true' if f['causal'] else 'false'}, true, {pipe}, true>(a, gr_flash_smem);
 }}
 """
     grid = f["lead"] * (N // f["BM"])
