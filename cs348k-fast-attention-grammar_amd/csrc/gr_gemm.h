@@ -14,10 +14,11 @@
 //    operand a 32-row block of A, both read from LDS as one 16-byte load per
 //    lane (8 consecutive k). The accumulators then give each lane one row m of
 //    C with 4-element runs along n, which are written as 8-byte stores.
-//  * LDS holds A as [BM][BK] and B^T as [BN][BK] (k contiguous). An [K, N]
-//    B is transposed on its way into LDS by packing pairs of k rows into
-//    dwords; a K-major B is copied as is. 16-byte chunks are XOR-swizzled by
-//    row so the MFMA operand reads and the tile writes are conflict free.
+//  * LDS holds A as [BM][BK] (k contiguous). A K-major B is held as [BN][BK];
+//    a [K, N] B as it is in memory, [BK][BN], its fragments read with
+//    gfx950's transposing LDS read (gr_tr_frag). 16-byte chunks are
+//    XOR-swizzled by row so the MFMA operand reads and the tile writes are
+//    conflict free.
 //  * Two LDS stages: the next k tile is fetched from global into registers
 //    while the current one feeds the MFMAs, then written to the other stage;
 //    one barrier per k tile.
@@ -101,7 +102,10 @@ __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
   T* C = static_cast<T*>(a.c) + z * a.c_sb + (long long)tm * BM * a.c_sm + (long long)tn * BN;
 
   gr_row_loader<T, BM, BK, NT, false> la;
-  typename gr_cond<B_KMAJOR, gr_row_loader<T, BN, BK, NT, false>, gr_tr_loader<T, BK, BN, NT, false>>::type lb;
+  // A [K, N] B is copied into LDS as laid out in memory ([BK][BN], swizzled for
+  // transposing reads) and its fragments are read back with gr_tr_frag; a
+  // K-major B is already [BN][BK].
+  typename gr_cond<B_KMAJOR, gr_row_loader<T, BN, BK, NT, false>, gr_row_loader<T, BK, BN, NT, false, true>>::type lb;
   la.init(tid, a.a_sm);
   lb.init(tid, a.b_s);
   const long long b_step = B_KMAJOR ? (long long)BK : (long long)BK * a.b_s;
@@ -133,7 +137,10 @@ __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
 #pragma unroll
       for (int i = 0; i < TN; ++i) {
         const int row = wn * G::WN + i * 32 + l32;
-        bt[i] = gr_as<vec8>(gr_ld16(cur + G::A_BYTES + row * (BK * 2) + gr_swz<CPR>(row, 2 * ks + g) * 16));
+        if constexpr (B_KMAJOR)
+          bt[i] = gr_as<vec8>(gr_ld16(cur + G::A_BYTES + row * (BK * 2) + gr_swz<CPR>(row, 2 * ks + g) * 16));
+        else
+          bt[i] = gr_tr_frag<T, BN, false>(cur + G::A_BYTES, ks * 16, wn * G::WN + i * 32, lane);
       }
 #pragma unroll
       for (int j = 0; j < TM; ++j) {
