@@ -121,6 +121,41 @@ struct gr_row_loader {
   }
 };
 
+// Global [ROWS][COLS] tile -> LDS rows, same shape and swizzle as
+// gr_row_loader, but loaded straight into LDS (gfx950 global_load_lds_dwordx4):
+// no staging registers and no LDS write instructions. Each such load writes
+// its 64 lanes' 16-byte chunks to 1 KiB of LDS at a wave-uniform base, lane l
+// at base + 16 l, so the swizzle is applied on the global side: the lane that
+// lands on LDS slot (row, physical chunk) fetches logical chunk swz(row,
+// physical chunk) (the XOR swizzles are involutions). The data is in LDS once
+// the wave's vmcnt drains; callers wait on it before the publishing barrier.
+template <class T, int ROWS, int COLS, int NT, bool TRSWZ = false>
+struct gr_lds_loader {
+  static constexpr int CPR = COLS / 8;
+  static constexpr int CHUNKS = ROWS * CPR;
+  static constexpr int PER = CHUNKS / NT;
+  static_assert(CHUNKS % NT == 0, "tile chunks must be a multiple of the thread count");
+  int goff[PER];
+  int lwave;
+  __device__ __forceinline__ void init(int tid, long long ld) {
+    lwave = (tid >> 6) * 64 * 16;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int c = tid + i * NT;
+      const int row = c / CPR, pc = c % CPR;
+      const int lc = TRSWZ ? gr_swz_tr<CPR>(row, pc) : gr_swz<CPR>(row, pc);
+      goff[i] = (int)(row * ld) + lc * 8;
+    }
+  }
+  __device__ __forceinline__ void load(const T* src, char* dst) const {
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(src + goff[i]),
+                                       (__attribute__((address_space(3))) void*)(dst + i * NT * 16 + lwave),
+                                       16, 0, 0);
+  }
+};
+
 // Global [SR][SC] tile (row stride ld) -> LDS [SC][SR] (transposed). Each unit
 // takes two source rows x 8 columns and writes 8 dwords, each holding the pair
 // of source-row values for one destination row.

@@ -27,6 +27,12 @@
 #pragma once
 #include "gr_flash_fwd.h"
 
+// Tiles are loaded straight into LDS (gr_lds_loader) unless built with
+// -DGR_GEMM_DIRECT=0, which stages them through registers (gr_row_loader).
+#ifndef GR_GEMM_DIRECT
+#define GR_GEMM_DIRECT 1
+#endif
+
 #ifndef GR_EPI_NONE
 #define GR_EPI_NONE 0
 #define GR_EPI_RELU 1
@@ -71,7 +77,7 @@ struct gr_gemm_cfg {
   static_assert(BK / 8 >= 2, "k tile");
 };
 
-template <class T, int BM, int BN, int BK, int WGM, int WGN, bool B_KMAJOR, int EPI>
+template <class T, int BM, int BN, int BK, int WGM, int WGN, bool B_KMAJOR, int EPI, bool DIRECT = GR_GEMM_DIRECT>
 __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
   typedef gr_mfma<T> MF;
   typedef typename MF::vec8 vec8;
@@ -101,13 +107,6 @@ __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
                (B_KMAJOR ? (long long)tn * BN * a.b_s : (long long)tn * BN);
   T* C = static_cast<T*>(a.c) + z * a.c_sb + (long long)tm * BM * a.c_sm + (long long)tn * BN;
 
-  gr_row_loader<T, BM, BK, NT, false> la;
-  // A [K, N] B is copied into LDS as laid out in memory ([BK][BN], swizzled for
-  // transposing reads) and its fragments are read back with gr_tr_frag; a
-  // K-major B is already [BN][BK].
-  typename gr_cond<B_KMAJOR, gr_row_loader<T, BN, BK, NT, false>, gr_row_loader<T, BK, BN, NT, false, true>>::type lb;
-  la.init(tid, a.a_sm);
-  lb.init(tid, a.b_s);
   const long long b_step = B_KMAJOR ? (long long)BK : (long long)BK * a.b_s;
 
   gr_f32x16 acc[TN][TM];
@@ -116,21 +115,8 @@ __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
 #pragma unroll
     for (int j = 0; j < TM; ++j) acc[i][j] = (gr_f32x16)(0.f);
 
-  const int nk = a.K / BK;
-  la.gload(A, tid);
-  lb.gload(B, tid);
-  la.sstore(lds, tid);
-  lb.sstore(lds + G::A_BYTES, tid);
-  __syncthreads();
-
-  for (int kt = 0; kt < nk; ++kt) {
-    const char* cur = lds + (kt & 1) * G::STAGE;
-    char* nxt = lds + ((kt + 1) & 1) * G::STAGE;
-    const bool more = kt + 1 < nk;
-    if (more) {
-      la.gload(A + (long long)(kt + 1) * BK, tid);
-      lb.gload(B + (long long)(kt + 1) * b_step, tid);
-    }
+  // one k tile of MFMAs from an LDS stage
+  auto mma_tile = [&](const char* cur) {
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       vec8 bt[TN], am[TM];
@@ -152,11 +138,59 @@ __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
 #pragma unroll
         for (int j = 0; j < TM; ++j) acc[i][j] = MF::mma32(bt[i], am[j], acc[i][j]);
     }
-    if (more) {
-      la.sstore(nxt, tid);
-      lb.sstore(nxt + G::A_BYTES, tid);
-    }
+  };
+
+  const int nk = a.K / BK;
+  if constexpr (DIRECT) {
+    // tiles go straight from global memory into the next LDS stage while the
+    // current one feeds the MFMAs; the stage is published after vmcnt drains
+    gr_lds_loader<T, BM, BK, NT> la;
+    typename gr_cond<B_KMAJOR, gr_lds_loader<T, BN, BK, NT>, gr_lds_loader<T, BK, BN, NT, true>>::type lb;
+    la.init(tid, a.a_sm);
+    lb.init(tid, a.b_s);
+    la.load(A, lds);
+    lb.load(B, lds + G::A_BYTES);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const char* cur = lds + (kt & 1) * G::STAGE;
+      char* nxt = lds + ((kt + 1) & 1) * G::STAGE;
+      if (kt + 1 < nk) {
+        la.load(A + (long long)(kt + 1) * BK, nxt);
+        lb.load(B + (long long)(kt + 1) * b_step, nxt + G::A_BYTES);
+      }
+      mma_tile(cur);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+  } else {
+    gr_row_loader<T, BM, BK, NT, false> la;
+    // A [K, N] B is copied into LDS as laid out in memory ([BK][BN], swizzled for
+    // transposing reads) and its fragments are read back with gr_tr_frag; a
+    // K-major B is already [BN][BK].
+    typename gr_cond<B_KMAJOR, gr_row_loader<T, BN, BK, NT, false>, gr_row_loader<T, BK, BN, NT, false, true>>::type lb;
+    la.init(tid, a.a_sm);
+    lb.init(tid, a.b_s);
+    la.gload(A, tid);
+    lb.gload(B, tid);
+    la.sstore(lds, tid);
+    lb.sstore(lds + G::A_BYTES, tid);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const char* cur = lds + (kt & 1) * G::STAGE;
+      char* nxt = lds + ((kt + 1) & 1) * G::STAGE;
+      const bool more = kt + 1 < nk;
+      if (more) {
+        la.gload(A + (long long)(kt + 1) * BK, tid);
+        lb.gload(B + (long long)(kt + 1) * b_step, tid);
+      }
+      mma_tile(cur);
+      if (more) {
+        la.sstore(nxt, tid);
+        lb.sstore(nxt + G::A_BYTES, tid);
+      }
+      __syncthreads();
+    }
   }
 
   // epilogue: lane (l32, g) of block (i, j) holds row m = wm*WM + 32j + l32 and
