@@ -88,6 +88,33 @@ __device__ __forceinline__ void gr_st16(void* p, gr_u32x4 v) {
   *reinterpret_cast<gr_u32x4*>(p) = v;
 }
 
+// 16 bytes per lane from global memory straight into LDS (gfx950
+// global_load_lds_dwordx4): lane l's bytes land at LDS address lds + 16 l,
+// where lds must be wave-uniform (it goes through M0; gr_lds_addr gives the
+// LDS address of a pointer into shared memory). Written as inline assembly so
+// that the compiler does not treat the load as an LDS store it must wait for
+// before every later LDS read (it cannot tell the slot being filled from the
+// slot being read); callers wait on vmcnt themselves before publishing the
+// tile. M0 is saved and restored around the load, and one wait state
+// separates the M0 write from the load that reads it.
+__device__ __forceinline__ void gr_g2lds16(const void* g, unsigned int lds) {
+  unsigned int saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(lds)
+      : "memory");
+}
+// LDS address of a (generic) pointer into shared memory: the low 32 bits of a
+// flat address in the LDS aperture.
+__device__ __forceinline__ unsigned int gr_lds_addr(const void* p) {
+  return (unsigned int)(unsigned long long)p;
+}
+
 // Exchange with the lane 32 positions away (the other half of the wavefront).
 __device__ __forceinline__ float gr_xor32(float v) {
   return __shfl_xor(v, 32, 64);

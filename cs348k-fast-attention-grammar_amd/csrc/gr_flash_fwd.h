@@ -127,32 +127,30 @@ struct gr_row_loader {
 // its 64 lanes' 16-byte chunks to 1 KiB of LDS at a wave-uniform base, lane l
 // at base + 16 l, so the swizzle is applied on the global side: the lane that
 // lands on LDS slot (row, physical chunk) fetches logical chunk swz(row,
-// physical chunk) (the XOR swizzles are involutions). The data is in LDS once
+// physical chunk) (the XOR swizzles are involutions); with PERM, LDS row r
+// holds global row gr_perm32(r) (also an involution). The data is in LDS once
 // the wave's vmcnt drains; callers wait on it before the publishing barrier.
-template <class T, int ROWS, int COLS, int NT, bool TRSWZ = false>
+template <class T, int ROWS, int COLS, int NT, bool TRSWZ = false, bool PERM = false>
 struct gr_lds_loader {
   static constexpr int CPR = COLS / 8;
   static constexpr int CHUNKS = ROWS * CPR;
   static constexpr int PER = CHUNKS / NT;
   static_assert(CHUNKS % NT == 0, "tile chunks must be a multiple of the thread count");
   int goff[PER];
-  int lwave;
+  unsigned int lwave;   // wave-uniform
   __device__ __forceinline__ void init(int tid, long long ld) {
-    lwave = (tid >> 6) * 64 * 16;
+    lwave = __builtin_amdgcn_readfirstlane((tid >> 6) * 64 * 16);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int c = tid + i * NT;
       const int row = c / CPR, pc = c % CPR;
       const int lc = TRSWZ ? gr_swz_tr<CPR>(row, pc) : gr_swz<CPR>(row, pc);
-      goff[i] = (int)(row * ld) + lc * 8;
+      goff[i] = (int)((PERM ? gr_perm32(row) : row) * ld) + lc * 8;
     }
   }
   __device__ __forceinline__ void load(const T* src, char* dst) const {
 #pragma unroll
-    for (int i = 0; i < PER; ++i)
-      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(src + goff[i]),
-                                       (__attribute__((address_space(3))) void*)(dst + i * NT * 16 + lwave),
-                                       16, 0, 0);
+    for (int i = 0; i < PER; ++i) gr_g2lds16(src + goff[i], gr_lds_addr(dst) + i * NT * 16 + lwave);
   }
 };
 
@@ -275,7 +273,8 @@ __device__ __forceinline__ void gr_flash_qk(gr_f32x16 (&s)[BN / 32][QB], const c
   }
 }
 
-template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT, bool PIPE, bool TR = false>
+template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT, bool PIPE, bool TR = false,
+          bool DIRECT = false>
 __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* lds) {
   typedef gr_mfma<T> MF;
   typedef typename MF::vec8 vec8;
@@ -333,8 +332,13 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
   typedef gr_row_loader<T, BN, D, NT, true> KRows;
   typedef typename gr_cond<KTR, gr_row_loader<T, D, BN, NT, false, true>, gr_tr_loader<T, D, BN, NT, true>>::type KCols;
   typedef typename gr_cond<TR, gr_row_loader<T, BN, D, NT, false, true>, gr_tr_loader<T, BN, D, NT, false>>::type VLoad;
-  typename gr_cond<KT_LAYOUT, KCols, KRows>::type kl;
-  VLoad vl;
+  // DIRECT (needs TR): the same tiles, loaded straight into LDS.
+  static_assert(!DIRECT || TR, "direct-to-LDS tiles are read through gr_tr_frag");
+  typedef typename gr_cond<KT_LAYOUT, gr_lds_loader<T, D, BN, NT, true>, gr_lds_loader<T, BN, D, NT, false, true>>::type
+      KDirect;
+  typedef gr_lds_loader<T, BN, D, NT, true> VDirect;
+  typename gr_cond<DIRECT, KDirect, typename gr_cond<KT_LAYOUT, KCols, KRows>::type>::type kl;
+  typename gr_cond<DIRECT, VDirect, VLoad>::type vl;
   kl.init(tid, a.k_sn);
   vl.init(tid, a.v_sn);
   // Element offset of key tile t in K (KT layout: a column offset).
@@ -351,13 +355,19 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
   // stores K_{t+2}, V_{t+1} into the slots K_t and V_{t-1} occupied. Without
   // PIPE iteration t reads K_t, V_t and stores K_{t+1}, V_{t+1}.
   constexpr int KAHEAD = PIPE ? 2 : 1;
-  kl.gload(Kp, tid);
-  vl.gload(Vp, tid);
-  kl.sstore(ks0, tid);
-  vl.sstore(vt0, tid);
-  if (PIPE && ntile > 1) {
-    kl.gload(Kp + k_tile, tid);
-    kl.sstore(ks0 + L::KS, tid);
+  if constexpr (DIRECT) {
+    kl.load(Kp, ks0);
+    vl.load(Vp, vt0);
+    if (PIPE && ntile > 1) kl.load(Kp + k_tile, ks0 + L::KS);
+  } else {
+    kl.gload(Kp, tid);
+    vl.gload(Vp, tid);
+    kl.sstore(ks0, tid);
+    vl.sstore(vt0, tid);
+    if (PIPE && ntile > 1) {
+      kl.gload(Kp + k_tile, tid);
+      kl.sstore(ks0 + L::KS, tid);
+    }
   }
   // Retire every prologue load (the Q fragments in particular) before the
   // loop: the compiler's wait-counter tracking cannot see through the loop
@@ -378,8 +388,17 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
   auto tile = [&](const int t, auto odd_tag, auto& s, auto& sn) {
     constexpr int ODD = decltype(odd_tag)::value;
     const bool pf_k = t + KAHEAD < ntile, pf_v = t + 1 < ntile;
-    if (pf_k) kl.gload(Kp + (t + KAHEAD) * k_tile, tid);
-    if (pf_v) vl.gload(Vp + (t + 1) * v_tile, tid);
+    // The slots the next tiles go to were last read before the previous
+    // iteration's closing barrier.
+    char* const k_next = ks0 + (PIPE ? ODD : (ODD ^ 1)) * L::KS;
+    char* const v_next = vt0 + (ODD ^ 1) * L::VT;
+    if constexpr (DIRECT) {
+      if (pf_k) kl.load(Kp + (t + KAHEAD) * k_tile, k_next);
+      if (pf_v) vl.load(Vp + (t + 1) * v_tile, v_next);
+    } else {
+      if (pf_k) kl.gload(Kp + (t + KAHEAD) * k_tile, tid);
+      if (pf_v) vl.gload(Vp + (t + 1) * v_tile, tid);
+    }
     const int k0 = t * BN;
     if (wave_active(t)) {
       if constexpr (!PIPE) gr_flash_qk<T, D, BN, QB, KTR>(s, ks0 + ODD * L::KS, qf, l32, g);
@@ -470,8 +489,12 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
         }
       }
     }
-    if (pf_k) kl.sstore(ks0 + (PIPE ? ODD : (ODD ^ 1)) * L::KS, tid);
-    if (pf_v) vl.sstore(vt0 + (ODD ^ 1) * L::VT, tid);
+    if constexpr (DIRECT) {
+      __builtin_amdgcn_s_waitcnt(0);   // this wave's tile loads have landed in LDS
+    } else {
+      if (pf_k) kl.sstore(k_next, tid);
+      if (pf_v) vl.sstore(v_next, tid);
+    }
     __syncthreads();
   };
 
@@ -520,10 +543,11 @@ struct gr_flash_wpe {
 
 // Kernel wrapper used by the prebuilt library; the grammar renderer emits its
 // own wrappers with baked-in shapes around the same body.
-template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT, bool PIPE, bool TR = false>
+template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT, bool PIPE, bool TR = false,
+          bool DIRECT = false>
 __global__ __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(gr_flash_wpe<D, BN, NW, QB, KT_LAYOUT, PIPE>::value)))
 void gr_flash_fwd_kernel(gr_attn_args a) {
   extern __shared__ __attribute__((aligned(16))) char gr_lds[];
-  gr_flash_fwd_body<T, D, BN, NW, QB, CAUSAL, KT_LAYOUT, PIPE, TR>(a, gr_lds);
+  gr_flash_fwd_body<T, D, BN, NW, QB, CAUSAL, KT_LAYOUT, PIPE, TR, DIRECT>(a, gr_lds);
 }
