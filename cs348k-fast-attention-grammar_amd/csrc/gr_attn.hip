@@ -14,34 +14,41 @@ template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT, bool PIP
 int launch_flash(const gr_attn_args& a, hipStream_t st) {
   constexpr int BM = NW * QB * 32;
   constexpr int LDS = gr_flash_lds<D, BN>::BYTES;
+  // K/V tiles go straight into LDS when every thread moves whole 16-byte
+  // chunks of them (D * BN / 8 chunks per tile), else through registers.
+  constexpr bool DIRECT = (D * BN / 8) % (NW * 64) == 0;
   if (a.N % BM != 0 || a.N % BN != 0)
     return gr::fail(GR_E_ARG, "gr_attn_fwd: N=%d must be a multiple of block_m=%d and block_n=%d", a.N, BM, BN);
   const long long nblk = (long long)a.B * a.H * (a.N / BM);
   if (nblk <= 0 || nblk > 0x7fffffffLL) return gr::fail(GR_E_ARG, "gr_attn_fwd: grid size %lld out of range", nblk);
-  hipLaunchKernelGGL((gr_flash_fwd_kernel<T, D, BN, NW, QB, CAUSAL, KT, PIPE, true>), dim3((unsigned)nblk), dim3(NW * 64), LDS,
-                     st, a);
+  hipLaunchKernelGGL((gr_flash_fwd_kernel<T, D, BN, NW, QB, CAUSAL, KT, PIPE, true, DIRECT>), dim3((unsigned)nblk),
+                     dim3(NW * 64), LDS, st, a);
   return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_fwd launch");
 }
 
 // Tile configurations compiled into the library: (block_m, block_n) ->
-// (waves, query blocks per wave, key tile).
+// (waves, query blocks per wave, key tile). One wave per 32 queries.
+// block_m 0 / block_n 0 pick the largest tiles that divide N (256 x 128 at
+// D = 64, 256 x 64 at D = 128).
 template <class T, int D, bool CAUSAL, bool KT>
 int dispatch_tiles(const gr_attn_args& a, int bm, int bn, hipStream_t st) {
-  if (bm == 0) bm = 128;
-  if (bn == 0) bn = 64;
+  if (bm == 0) bm = a.N % 256 == 0 ? 256 : a.N % 128 == 0 ? 128 : 64;
+  if (bn == 0) bn = (D == 64 && a.N % 128 == 0) ? 128 : a.N % 64 == 0 ? 64 : 32;
+  if (bm == 256 && bn == 64) return launch_flash<T, D, 64, 8, 1, CAUSAL, KT>(a, st);
+  if (bm == 256 && bn == 32) return launch_flash<T, D, 32, 8, 1, CAUSAL, KT>(a, st);
   if (bm == 128 && bn == 64) return launch_flash<T, D, 64, 4, 1, CAUSAL, KT>(a, st);
   if (bm == 128 && bn == 32) return launch_flash<T, D, 32, 4, 1, CAUSAL, KT>(a, st);
   if (bm == 64 && bn == 64) return launch_flash<T, D, 64, 2, 1, CAUSAL, KT>(a, st);
+  if (bm == 64 && bn == 32) return launch_flash<T, D, 32, 2, 1, CAUSAL, KT>(a, st);
   // block_m = 129 / 257 select the software-pipelined schedule (128 / 256 queries).
   if (bm == 129 && bn == 64) return launch_flash<T, D, 64, 4, 1, CAUSAL, KT, true>(a, st);
   if (bm == 129 && bn == 32) return launch_flash<T, D, 32, 4, 1, CAUSAL, KT, true>(a, st);
+  if (bm == 257 && bn == 64) return launch_flash<T, D, 64, 8, 1, CAUSAL, KT, true>(a, st);
+  if (bm == 257 && bn == 32) return launch_flash<T, D, 32, 8, 1, CAUSAL, KT, true>(a, st);
   if constexpr (D == 64) {
+    if (bm == 256 && bn == 128) return launch_flash<T, D, 128, 8, 1, CAUSAL, KT>(a, st);
     if (bm == 128 && bn == 128) return launch_flash<T, D, 128, 4, 1, CAUSAL, KT>(a, st);
-    if (bm == 256 && bn == 64) return launch_flash<T, D, 64, 4, 2, CAUSAL, KT>(a, st);
-    if (bm == 256 && bn == 32) return launch_flash<T, D, 32, 4, 2, CAUSAL, KT>(a, st);
     if (bm == 129 && bn == 128) return launch_flash<T, D, 128, 4, 1, CAUSAL, KT, true>(a, st);
-    if (bm == 257 && bn == 64) return launch_flash<T, D, 64, 4, 2, CAUSAL, KT, true>(a, st);
-    if (bm == 257 && bn == 32) return launch_flash<T, D, 32, 4, 2, CAUSAL, KT, true>(a, st);
   }
   return gr::fail(GR_E_ARG, "gr_attn_fwd: unsupported tile (block_m=%d, block_n=%d) for D=%d", bm, bn, D);
 }

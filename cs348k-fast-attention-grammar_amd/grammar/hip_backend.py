@@ -79,7 +79,7 @@ def _flt(x: float) -> str:
 # ---------------------------------------------------------------------------
 # Flash lowering
 # ---------------------------------------------------------------------------
-FLASH_BM = {32: (1, 1), 64: (2, 1), 128: (4, 1), 256: (4, 2)}   # block_m -> (waves, query blocks/wave)
+FLASH_BM = {32: (1, 1), 64: (2, 1), 128: (4, 1), 256: (8, 1)}   # block_m -> (waves, query blocks/wave)
 
 
 FLASH_DEFAULT_BN = {64: 128, 128: 64}    # key tile when the stage does not tile the key axis
@@ -223,6 +223,8 @@ def _render_flash(loop, program, f) -> tuple:
     N, D = f["N"], f["D"]
     pipe = "false"
     nt = f["NW"] * 64
+    # K^T / V tiles straight into LDS when each thread moves whole 16-byte chunks
+    direct = "true" if (D * f["BN"] // 8) % nt == 0 else "false"
     code = f"""
 // stage {loop.out}: flash attention (online softmax over key tiles of {f['BN']}, {f['BM']} queries/workgroup)
 extern "C" __global__ __launch_bounds__({nt})
@@ -237,7 +239,7 @@ void {kname}({params}) {{
   a.o_sb = {N * D}LL; a.o_sh = 0; a.o_sn = {D};
   a.B = {f['lead']}; a.H = 1; a.N = {N};
   a.scale_log2 = {_flt(f['scale'] * LOG2E)};
-  gr_flash_fwd_body<{T}, {D}, {f['BN']}, {f['NW']}, {f['QB']}, {'true' if f['causal'] else 'false'}, true, {pipe}, true>(a, gr_flash_smem);
+  gr_flash_fwd_body<{T}, {D}, {f['BN']}, {f['NW']}, {f['QB']}, {'true' if f['causal'] else 'false'}, true, {pipe}, true, {direct}>(a, gr_flash_smem);
 }}
 """
     grid = f["lead"] * (N // f["BM"])

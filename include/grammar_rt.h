@@ -106,8 +106,11 @@ int gr_plan_time(gr_plan* p, void* stream, int warmup, int iters, int mode, floa
  *  (unit stride along D). K: [B, H, N, D] if k_transposed == 0, else KT
  *  [B, H, D, N] whose k_strides = {batch, head, d} (unit stride along N).
  *  D in {64, 128}; N a multiple of block_m and block_n.
- *  block_m: queries per workgroup (0 = default), block_n: keys per tile
- *  (0 = default). */
+ *  block_m: queries per workgroup, 64 / 128 / 256 (one wave per 32 queries;
+ *  129 / 257: 128 / 256 with the software-pipelined schedule), 0 = the
+ *  largest of 256 / 128 / 64 dividing N. block_n: keys per tile, 32 / 64 /
+ *  128 (128 at D = 64 only), 0 = 128 at D = 64 when it divides N, else 64
+ *  or 32. */
 int gr_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H,
                 int N, int D, const long long* q_strides, const long long* k_strides,
                 const long long* v_strides, const long long* o_strides, int k_transposed,

@@ -63,6 +63,13 @@ SMALL = [
     (1, 2, 512, 64, "fp16", False, False, 64, 64),
     (1, 2, 512, 64, "fp16", True, False, 256, 64),
     (1, 2, 512, 64, "bf16", False, True, 256, 32),
+    (1, 2, 512, 64, "fp16", False, True, 256, 128),
+    (1, 2, 512, 64, "bf16", True, True, 256, 128),
+    (2, 3, 512, 128, "fp16", False, True, 256, 64),
+    (1, 2, 512, 128, "bf16", True, False, 256, 32),
+    (1, 2, 256, 64, "fp16", True, True, 64, 32),
+    (1, 2, 384, 64, "fp16", False, False, 0, 0),
+    (1, 2, 320, 128, "bf16", True, True, 0, 0),
     (1, 2, 512, 128, "bf16", True, True, 128, 32),
     (1, 1, 128, 64, "fp16", True, False, 128, 64),
     # block_m 129 / 257: the software-pipelined schedule (next tile's scores
@@ -72,6 +79,7 @@ SMALL = [
     (1, 2, 512, 64, "fp16", True, True, 257, 64),
     (1, 2, 512, 64, "bf16", False, False, 257, 32),
     (1, 2, 512, 128, "fp16", True, True, 129, 32),
+    (1, 2, 512, 128, "bf16", False, True, 257, 64),
     (1, 1, 128, 64, "fp16", False, False, 129, 128),
 ]
 
