@@ -153,3 +153,21 @@ class HipModule:
 
 def load_module(src: str) -> HipModule:
     return HipModule(src)
+
+
+def save_best(path: str, program, doc: str, best_loss_ms: float, iterations: int, stats: dict) -> dict:
+    """Write a descent's best program as JSON: its structural key (rebuilt by
+    kernel_ast.program_from_key), stage tiles and the lowering the HIP
+    renderer picks for each stage (no compile). `stats` is Evaluator.stats()."""
+    import json
+    from .kernel_ast import emit_module, structural_key
+    plan = parse_plan(emit_module(program))
+    rec = {"_doc": doc, "best_loss_ms": best_loss_ms, "iterations": iterations,
+           "evals_per_min": stats.get("evals_per_min"), "timed_variants": stats.get("timed_variants"),
+           "stages": [[loop.out, list(loop.tile_shape)] for loop in program.body],
+           "lowering": [[st["kernel"], st["lowering"], st.get("tiles")] for st in plan["steps"]],
+           "key": json.loads(json.dumps(structural_key(program)))}
+    with open(path, "w") as f:
+        json.dump(rec, f)
+        f.write("\n")
+    return rec

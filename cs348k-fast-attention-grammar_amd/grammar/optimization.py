@@ -688,7 +688,12 @@ def stage2_step(program: Program, ev: Evaluator, K: int, rules, rng: random.Rand
                                   mem_precondition=(0 if ev.cfg.repairable else ev.cfg.mem_budget))
         if not menu:
             break
-        sample = rng.sample(menu, min(K, len(menu)))
+        # While the program is still over the memory budget (a penalty, not a
+        # time) every applicable rewrite is ranked instead of K sampled ones:
+        # such candidates are mostly rejected statically (no compile), and a
+        # random K can keep missing the one fusion that reaches a feasible
+        # program, leaving the walk among penalties that differ in bytes only.
+        sample = list(menu) if cur >= MEM_PENALTY_BASE else rng.sample(menu, min(K, len(menu)))
         if log:
             print(f"===== it {it} | STAGE 2: ranking {len(sample)} rewrite(s), base loss {cur:.4g} =====", flush=True)
         best = None

@@ -42,3 +42,20 @@ def test_committed_best_programs_rebuild():
     assert lowerings["attn_c2_best.json"] == ["flash"]
     assert lowerings["attn_c3_best.json"] == ["flash"]
     assert lowerings["mlp_c4_best.json"] == ["gemm", "gemm"]
+
+
+def test_save_best_round_trip(tmp_path):
+    # the --save-best writer of the search drivers reproduces a committed file's
+    # key, stage tiles and (renderer-chosen) lowering
+    sys.path.insert(0, os.path.join(REPO, "cs348k-fast-attention-grammar_amd"))
+    from grammar.hip_module import save_best
+    from grammar.kernel_ast import program_from_key
+    saved = json.load(open(os.path.join(REPO, "cs348k-fast-attention-grammar_amd", "runs", "mlp_c4_best.json")))
+    out = tmp_path / "best.json"
+    rec = save_best(str(out), program_from_key(saved["key"]), "doc", 1.0, 7,
+                    {"evals_per_min": 2.0, "timed_variants": 3})
+    again = json.load(open(out))
+    assert again == rec
+    assert again["key"] == saved["key"] and again["stages"] == saved["stages"]
+    assert [lw[:2] for lw in again["lowering"]] == [lw[:2] for lw in saved["lowering"]]
+    assert (again["best_loss_ms"], again["iterations"], again["timed_variants"]) == (1.0, 7, 3)
