@@ -471,7 +471,51 @@ def stage1_sweep(program: Program, ev: Evaluator, ladder: tuple | None = None, c
         best = best_loss
         if neighbor and not use_neighbor and best < MEM_PENALTY_BASE:
             use_neighbor = True
+    if full_ladder_for and best >= MEM_PENALTY_BASE:
+        best = _joint_sweep(prog, params, full_ladder_for, ev, best)
     return prog, best
+
+
+JOINT_MAX = 256   # tile combinations per stage in a joint sweep
+
+
+def _joint_sweep(prog: Program, params: list, stages: set, ev: Evaluator, best: float) -> float:
+    """Every combination of the tile parameters of each changed stage, tried
+    when the coordinate sweep left the program over the memory budget. A
+    stage whose lowering needs two tiles to change together (the flash kernel
+    wants both its row tile in its ladder and the full head dim) cannot be
+    reached one coordinate at a time from tiles a penalty shrank."""
+    import itertools
+    for stage in sorted(stages):
+        sp = [p for p in params if _param_stage(p.name) == stage]
+        if len(sp) < 2:
+            continue
+        grids = [sorted(set(p.ladder()) | {p.current}) for p in sp]
+        if math.prod(len(g) for g in grids) > JOINT_MAX:
+            continue
+        cur = [p.current for p in sp]
+        combos, snaps = [], []
+        for combo in itertools.product(*grids):
+            if list(combo) == cur:
+                continue
+            for p, v in zip(sp, combo):
+                p.set(v)
+            snap = R.clone_program(prog)
+            R._strip_clone_meta(snap)
+            combos.append(combo)
+            snaps.append(snap)
+        for p, v in zip(sp, cur):
+            p.set(v)
+        ev.prefetch(snaps)
+        pick = None
+        for combo, snap in zip(combos, snaps):
+            loss = ev(snap)
+            if loss < best:
+                best, pick = loss, combo
+        if pick is not None:
+            for p, v in zip(sp, pick):
+                p.set(v)
+    return best
 
 
 # ---------------------------------------------------------------------------
