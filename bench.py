@@ -197,7 +197,7 @@ def main() -> int:
     ap.add_argument("--no-mlp", action="store_true")
     ap.add_argument("--no-side", action="store_true",
                     help="skip the committed descent-found C3 / C4 programs")
-    ap.add_argument("--block-m", type=int, default=128, help="hand-written kernel: queries per workgroup")
+    ap.add_argument("--block-m", type=int, default=256, help="hand-written kernel: queries per workgroup")
     ap.add_argument("--block-n", type=int, default=128, help="hand-written kernel: keys per tile")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run --steps plain device copies of MIB MiB "
@@ -210,7 +210,7 @@ def main() -> int:
         return 2
 
     import torch
-    from grammar.attention import flash_attention_fwd
+    from grammar.attention import bind_flash_attention
     from grammar.workloads import CONFIGS, attention_inputs
 
     if not torch.cuda.is_available():
@@ -261,11 +261,8 @@ def main() -> int:
         traffic_key = (f"{cfg.name}:{cfg.dtype}:{main_k['lowering']}:"
                        f"bm{(main_k.get('tiles') or {}).get('block_m')}:bn{(main_k.get('tiles') or {}).get('block_n')}")
     else:
-        out_t = torch.empty_like(q)
+        step, out_t = bind_flash_attention(q, k, v, causal=cfg.causal, block_m=args.block_m, block_n=args.block_n)
         kernel = {"name": "gr_flash_fwd (hand-written)", "block_m": args.block_m, "block_n": args.block_n}
-
-        def step():
-            flash_attention_fwd(q, k, v, causal=cfg.causal, out=out_t, block_m=args.block_m, block_n=args.block_n)
         traffic_key = f"{cfg.name}:{cfg.dtype}:flash:bm{args.block_m}:bn{args.block_n}"
 
     # 2. the timed region
@@ -287,9 +284,9 @@ def main() -> int:
     # 3. side measurements
     hand = None
     if args.kernel == "descent":
-        o2 = torch.empty_like(q)
-        hms = timed(lambda: flash_attention_fwd(q, k, v, causal=cfg.causal, out=o2, block_m=args.block_m,
-                                                block_n=args.block_n), args.steps, args.warmup)
+        hand_launch, _ = bind_flash_attention(q, k, v, causal=cfg.causal, block_m=args.block_m,
+                                              block_n=args.block_n)
+        hms = timed(hand_launch, args.steps, args.warmup)
         hand = {"block_m": args.block_m, "block_n": args.block_n, "ms_per_step": round(hms, 6),
                 "tflops": round(cfg.flops / (hms * 1e-3) / 1e12, 3)}
         log(f"[bench] hand-written gr_attn_fwd: {hms * 1e3:.2f} us/step  {hand['tflops']:.1f} TFLOP/s")

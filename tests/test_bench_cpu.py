@@ -19,7 +19,7 @@ def test_measured_traffic_uses_calibrated_counters():
     sys.path.insert(0, REPO)
     import bench
     t = json.load(open(os.path.join(REPO, "profiles", "traffic.json")))
-    key = "C2:fp16:flash:bm128:bn64"
+    key = "C2:fp16:flash:bm256:bn128"
     k, c = t["kernels"][key], t["calibration"]
     want = int((k["fetch_kib"] * c["fetch_factor"] + k["write_kib"] * c["write_factor"]) * 1024)
     assert bench.measured_traffic(key) == want
