@@ -164,6 +164,36 @@ def side_programs(steps: int, seed: int) -> dict:
     return out
 
 
+def sdpa_reference(steps: int, seed: int) -> dict:
+    """torch's fused SDPA kernels (flash and memory-efficient backends only,
+    never the math path) at C2 and C3: the reference point the reference
+    quotes from flash-attn2-sota.py:41-62, reported, not built on."""
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    from grammar.workloads import CONFIGS, attention_inputs
+    out = {}
+    for name in ("C2", "C3"):
+        cfg = CONFIGS[name]
+        q, k, v = (t.to("cuda") for t in attention_inputs(cfg, seed=seed))
+        best = None
+        for be in (SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION):
+            try:
+                with sdpa_kernel([be]):
+                    ms = timed(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=cfg.causal),
+                               max(5, steps // (4 if name == "C2" else 20)), 3)
+            except RuntimeError as e:   # backend not built for this shape / dtype
+                log(f"[bench] sdpa {name} {be.name}: unavailable ({str(e)[:80]})")
+                continue
+            rec = {"backend": be.name, "ms": round(ms, 5), "tflops": round(cfg.flops / (ms * 1e-3) / 1e12, 2)}
+            if best is None or rec["ms"] < best["ms"]:
+                best = rec
+        out[name] = best
+        if best:
+            log(f"[bench] torch SDPA {name} ({best['backend']}): {best['ms']:.4f} ms  {best['tflops']:.1f} TFLOP/s")
+        del q, k, v
+    return out
+
+
 def run_descent(cfg, seconds: float, seed: int):
     """The rewrite descent from the naive program for at most `seconds`."""
     import run_attention_search as RS
@@ -196,7 +226,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-mlp", action="store_true")
     ap.add_argument("--no-side", action="store_true",
-                    help="skip the committed descent-found C3 / C4 programs")
+                    help="skip the committed descent-found C3 / C4 programs and the torch SDPA reference point")
     ap.add_argument("--block-m", type=int, default=256, help="hand-written kernel: queries per workgroup")
     ap.add_argument("--block-n", type=int, default=128, help="hand-written kernel: keys per tile")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -305,6 +335,7 @@ def main() -> int:
         del x, w1, w2, hbuf, y
 
     side = None if args.no_side else side_programs(args.steps, args.seed)
+    sdpa = None if args.no_side else sdpa_reference(args.steps, args.seed)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -342,6 +373,7 @@ def main() -> int:
         "handwritten": hand,
         "mlp_c4": mlp,
         "descent_programs": side,
+        "torch_sdpa": sdpa,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

@@ -14,8 +14,8 @@ template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT, bool PIP
 int launch_flash(const gr_attn_args& a, hipStream_t st) {
   constexpr int BM = NW * QB * 32;
   constexpr int LDS = gr_flash_lds<D, BN>::BYTES;
-  // K/V tiles go straight into LDS when every thread moves whole 16-byte
-  // chunks of them (D * BN / 8 chunks per tile), else through registers.
+  // K/V tiles go straight into LDS when they give every thread the same
+  // number of 16-byte chunks (D * BN / 8 per tile), else through registers.
   constexpr bool DIRECT = (D * BN / 8) % (NW * 64) == 0;
   if (a.N % BM != 0 || a.N % BN != 0)
     return gr::fail(GR_E_ARG, "gr_attn_fwd: N=%d must be a multiple of block_m=%d and block_n=%d", a.N, BM, BN);

@@ -134,23 +134,28 @@ template <class T, int ROWS, int COLS, int NT, bool TRSWZ = false, bool PERM = f
 struct gr_lds_loader {
   static constexpr int CPR = COLS / 8;
   static constexpr int CHUNKS = ROWS * CPR;
-  static constexpr int PER = CHUNKS / NT;
-  static_assert(CHUNKS % NT == 0, "tile chunks must be a multiple of the thread count");
+  static constexpr int PER = (CHUNKS + NT - 1) / NT;
   int goff[PER];
   unsigned int lwave;   // wave-uniform
-  __device__ __forceinline__ void init(int tid, long long ld) {
+  // rows_valid / chunks_valid (edge tiles): source rows and 16-byte chunks
+  // past them are read from the last valid one instead (the LDS tile is full,
+  // its extra rows / columns hold copies that the caller never stores).
+  __device__ __forceinline__ void init(int tid, long long ld, int rows_valid = ROWS, int chunks_valid = CPR) {
     lwave = __builtin_amdgcn_readfirstlane((tid >> 6) * 64 * 16);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int c = tid + i * NT;
       const int row = c / CPR, pc = c % CPR;
       const int lc = TRSWZ ? gr_swz_tr<CPR>(row, pc) : gr_swz<CPR>(row, pc);
-      goff[i] = (int)((PERM ? gr_perm32(row) : row) * ld) + lc * 8;
+      const int srow = PERM ? gr_perm32(row) : row;
+      goff[i] = (int)((srow < rows_valid ? srow : rows_valid - 1) * ld) + (lc < chunks_valid ? lc : chunks_valid - 1) * 8;
     }
   }
   __device__ __forceinline__ void load(const T* src, char* dst) const {
 #pragma unroll
-    for (int i = 0; i < PER; ++i) gr_g2lds16(src + goff[i], gr_lds_addr(dst) + i * NT * 16 + lwave);
+    for (int i = 0; i < PER; ++i)
+      if (CHUNKS % NT == 0 || (int)threadIdx.x + i * NT < CHUNKS)   // idle lanes write nothing
+        gr_g2lds16(src + goff[i], gr_lds_addr(dst) + i * NT * 16 + lwave);
   }
 };
 

@@ -19,19 +19,16 @@
 //    gfx950's transposing LDS read (gr_tr_frag). 16-byte chunks are
 //    XOR-swizzled by row so the MFMA operand reads and the tile writes are
 //    conflict free.
-//  * Two LDS stages: the next k tile is fetched from global into registers
-//    while the current one feeds the MFMAs, then written to the other stage;
-//    one barrier per k tile.
+//  * Two LDS stages: the next k tile goes straight from global memory into
+//    one stage (global_load_lds, no staging registers) while the current one
+//    feeds the MFMAs; one barrier per k tile.
 //  * Tiles are walked in groups of GROUP_M tile rows (B columns reused from
 //    L2), and the group order is remapped so consecutive groups run on one XCD.
+//  * M and N need not be multiples of the tile (N a multiple of 8): edge
+//    tiles read their last valid row / 16-byte column chunk in place of the
+//    missing ones and store only the valid part. K is a multiple of BK.
 #pragma once
 #include "gr_flash_fwd.h"
-
-// Tiles are loaded straight into LDS (gr_lds_loader) unless built with
-// -DGR_GEMM_DIRECT=0, which stages them through registers (gr_row_loader).
-#ifndef GR_GEMM_DIRECT
-#define GR_GEMM_DIRECT 1
-#endif
 
 #ifndef GR_EPI_NONE
 #define GR_EPI_NONE 0
@@ -77,7 +74,7 @@ struct gr_gemm_cfg {
   static_assert(BK / 8 >= 2, "k tile");
 };
 
-template <class T, int BM, int BN, int BK, int WGM, int WGN, bool B_KMAJOR, int EPI, bool DIRECT = GR_GEMM_DIRECT>
+template <class T, int BM, int BN, int BK, int WGM, int WGN, bool B_KMAJOR, int EPI>
 __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
   typedef gr_mfma<T> MF;
   typedef typename MF::vec8 vec8;
@@ -90,7 +87,7 @@ __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
   const int wm = wave / WGN, wn = wave % WGN;
 
   // tile walk: grouped rows, XCD-local groups
-  const int tiles_m = a.M / BM, tiles_n = a.N / BN;
+  const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
   const int ntile = tiles_m * tiles_n;
   const int bid = gr_xcd_remap(blockIdx.x, ntile);
   const int per_group = GROUP_M * tiles_n;
@@ -108,6 +105,9 @@ __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
   T* C = static_cast<T*>(a.c) + z * a.c_sb + (long long)tm * BM * a.c_sm + (long long)tn * BN;
 
   const long long b_step = B_KMAJOR ? (long long)BK : (long long)BK * a.b_s;
+  // valid rows of this tile of C and valid 16-byte chunks of its rows
+  const int rows_ok = a.M - tm * BM < BM ? a.M - tm * BM : BM;
+  const int cols_ok = a.N - tn * BN < BN ? a.N - tn * BN : BN;
 
   gr_f32x16 acc[TN][TM];
 #pragma unroll
@@ -140,57 +140,31 @@ __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
     }
   };
 
+  // tiles go straight from global memory into the next LDS stage while the
+  // current one feeds the MFMAs; the stage is published after vmcnt drains
   const int nk = a.K / BK;
-  if constexpr (DIRECT) {
-    // tiles go straight from global memory into the next LDS stage while the
-    // current one feeds the MFMAs; the stage is published after vmcnt drains
-    gr_lds_loader<T, BM, BK, NT> la;
-    typename gr_cond<B_KMAJOR, gr_lds_loader<T, BN, BK, NT>, gr_lds_loader<T, BK, BN, NT, true>>::type lb;
-    la.init(tid, a.a_sm);
-    lb.init(tid, a.b_s);
-    la.load(A, lds);
-    lb.load(B, lds + G::A_BYTES);
+  gr_lds_loader<T, BM, BK, NT> la;
+  // A [K, N] B is copied into LDS as laid out in memory ([BK][BN], swizzled for
+  // transposing reads) and its fragments are read back with gr_tr_frag; a
+  // K-major B is already [BN][BK].
+  typename gr_cond<B_KMAJOR, gr_lds_loader<T, BN, BK, NT>, gr_lds_loader<T, BK, BN, NT, true>>::type lb;
+  la.init(tid, a.a_sm, rows_ok);
+  if constexpr (B_KMAJOR) lb.init(tid, a.b_s, cols_ok);
+  else lb.init(tid, a.b_s, BK, cols_ok / 8);
+  la.load(A, lds);
+  lb.load(B, lds + G::A_BYTES);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const char* cur = lds + (kt & 1) * G::STAGE;
+    char* nxt = lds + ((kt + 1) & 1) * G::STAGE;
+    if (kt + 1 < nk) {
+      la.load(A + (long long)(kt + 1) * BK, nxt);
+      lb.load(B + (long long)(kt + 1) * b_step, nxt + G::A_BYTES);
+    }
+    mma_tile(cur);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-      const char* cur = lds + (kt & 1) * G::STAGE;
-      char* nxt = lds + ((kt + 1) & 1) * G::STAGE;
-      if (kt + 1 < nk) {
-        la.load(A + (long long)(kt + 1) * BK, nxt);
-        lb.load(B + (long long)(kt + 1) * b_step, nxt + G::A_BYTES);
-      }
-      mma_tile(cur);
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-    }
-  } else {
-    gr_row_loader<T, BM, BK, NT, false> la;
-    // A [K, N] B is copied into LDS as laid out in memory ([BK][BN], swizzled for
-    // transposing reads) and its fragments are read back with gr_tr_frag; a
-    // K-major B is already [BN][BK].
-    typename gr_cond<B_KMAJOR, gr_row_loader<T, BN, BK, NT, false>, gr_row_loader<T, BK, BN, NT, false, true>>::type lb;
-    la.init(tid, a.a_sm);
-    lb.init(tid, a.b_s);
-    la.gload(A, tid);
-    lb.gload(B, tid);
-    la.sstore(lds, tid);
-    lb.sstore(lds + G::A_BYTES, tid);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-      const char* cur = lds + (kt & 1) * G::STAGE;
-      char* nxt = lds + ((kt + 1) & 1) * G::STAGE;
-      const bool more = kt + 1 < nk;
-      if (more) {
-        la.gload(A + (long long)(kt + 1) * BK, tid);
-        lb.gload(B + (long long)(kt + 1) * b_step, tid);
-      }
-      mma_tile(cur);
-      if (more) {
-        la.sstore(nxt, tid);
-        lb.sstore(nxt + G::A_BYTES, tid);
-      }
-      __syncthreads();
-    }
   }
 
   // epilogue: lane (l32, g) of block (i, j) holds row m = wm*WM + 32j + l32 and
@@ -223,19 +197,18 @@ __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
     if (CHUNKS % NT == 0 || cidx < CHUNKS) {
       const int row = cidx / OCPR, cc = cidx % OCPR;
       const gr_u32x4 v = gr_ld16(lds + row * (BN * 2) + gr_swz<OCPR>(row, cc) * 16);
-      gr_st16(C + (long long)row * a.c_sm + cc * 8, v);
+      if (row < rows_ok && cc * 8 < cols_ok) gr_st16(C + (long long)row * a.c_sm + cc * 8, v);
     }
   }
 }
 
 // Waves per SIMD that the register budget allows for a wave tile of TN x TM
 // 32x32 blocks: 16*TN*TM accumulators plus 4*(TN+TM) operand registers,
-// loader staging and addressing.
+// loader offsets and addressing.
 template <int BM, int BN, int BK, int WGM, int WGN, bool B_KMAJOR>
 struct gr_gemm_wpe {
   typedef gr_gemm_cfg<BM, BN, BK, WGM, WGN> G;
-  static constexpr int LOADER = 4 * ((BM * BK / 8 + G::NT - 1) / G::NT) +
-                                (B_KMAJOR ? 4 : 8) * ((BN * BK / 8 + G::NT - 1) / G::NT);
+  static constexpr int LOADER = (BM * BK / 8 + G::NT - 1) / G::NT + (BN * BK / 8 + G::NT - 1) / G::NT;
   static constexpr int EST = 16 * G::TN * G::TM + 4 * (G::TN + G::TM) + LOADER + 40;
   static constexpr int value = EST > 240 ? 1 : 2;
 };

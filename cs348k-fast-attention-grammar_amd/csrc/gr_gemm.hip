@@ -13,10 +13,9 @@ namespace {
 template <class T, int BM, int BN, int BK, int WGM, int WGN, bool KM, int EPI>
 int launch_gemm(const gr_gemm_args& a, int batch, hipStream_t st) {
   typedef gr_gemm_cfg<BM, BN, BK, WGM, WGN> G;
-  if (a.M % BM || a.N % BN || a.K % BK)
-    return gr::fail(GR_E_ARG, "gr_gemm: M=%d N=%d K=%d must be multiples of the tile %dx%dx%d", a.M, a.N, a.K, BM,
-                    BN, BK);
-  const long long nblk = (long long)(a.M / BM) * (a.N / BN);
+  if (a.K % BK)
+    return gr::fail(GR_E_ARG, "gr_gemm: K=%d must be a multiple of the k tile %d", a.K, BK);
+  const long long nblk = (long long)((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   if (nblk <= 0 || nblk > 0x7fffffffLL || batch > 65535)
     return gr::fail(GR_E_ARG, "gr_gemm: grid (%lld tiles, batch %d) out of range", nblk, batch);
   hipLaunchKernelGGL((gr_gemm_kernel<T, BM, BN, BK, WGM, WGN, KM, EPI>), dim3((unsigned)nblk, (unsigned)batch),
@@ -24,15 +23,21 @@ int launch_gemm(const gr_gemm_args& a, int batch, hipStream_t st) {
   return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_gemm launch");
 }
 
-// (block_m, block_n) -> (k tile, wave grid) compiled into the library.
+// (block_m, block_n) -> (k tile, wave grid) compiled into the library; the
+// 128x128 and 256x256 tiles take 64-deep k tiles when K allows, else 32.
 template <class T, bool KM, int EPI>
 int dispatch_tile(const gr_gemm_args& a, int batch, int bm, int bn, hipStream_t st) {
   if (bm == 0) bm = 256;
   if (bn == 0) bn = 256;
-  if (bm == 128 && bn == 128) return launch_gemm<T, 128, 128, 64, 2, 2, KM, EPI>(a, batch, st);
+  const bool k64 = a.K % 64 == 0;
+  if (bm == 128 && bn == 128)
+    return k64 ? launch_gemm<T, 128, 128, 64, 2, 2, KM, EPI>(a, batch, st)
+               : launch_gemm<T, 128, 128, 32, 2, 2, KM, EPI>(a, batch, st);
   if (bm == 256 && bn == 128) return launch_gemm<T, 256, 128, 32, 2, 2, KM, EPI>(a, batch, st);
   if (bm == 128 && bn == 256) return launch_gemm<T, 128, 256, 32, 2, 2, KM, EPI>(a, batch, st);
-  if (bm == 256 && bn == 256) return launch_gemm<T, 256, 256, 64, 2, 4, KM, EPI>(a, batch, st);
+  if (bm == 256 && bn == 256)
+    return k64 ? launch_gemm<T, 256, 256, 64, 2, 4, KM, EPI>(a, batch, st)
+               : launch_gemm<T, 256, 256, 32, 2, 4, KM, EPI>(a, batch, st);
   return gr::fail(GR_E_ARG, "gr_gemm: unsupported tile (block_m=%d, block_n=%d)", bm, bn);
 }
 
@@ -59,6 +64,8 @@ extern "C" int gr_gemm(const void* a, const void* b, void* c, int dtype, int bat
                        int b_kmajor, int epilogue, float alpha, int block_m, int block_n, void* stream) {
   if (!a || !b || !c || !a_strides || !b_strides || !c_strides) return gr::fail(GR_E_ARG, "gr_gemm: null argument");
   if (batch <= 0 || M <= 0 || N <= 0 || K <= 0) return gr::fail(GR_E_ARG, "gr_gemm: sizes must be positive");
+  if (N % 8 != 0 || K % 32 != 0)
+    return gr::fail(GR_E_ARG, "gr_gemm: N=%d must be a multiple of 8 and K=%d a multiple of 32", N, K);
   if (!aligned16(a) || !aligned16(b) || !aligned16(c))
     return gr::fail(GR_E_ARG, "gr_gemm: base pointers must be 16-byte aligned");
   const long long* all[3] = {a_strides, b_strides, c_strides};

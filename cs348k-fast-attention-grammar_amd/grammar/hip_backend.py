@@ -354,7 +354,7 @@ def _match_gemm(loop: ParallelLoop, program: Program):
     if any(t != 1 for t in tile[:nb]):
         return None
     BM, BN = tile[nb], tile[nb + 1]
-    if BM not in GEMM_WAVES_M or BN not in GEMM_WAVES_N or M % BM or N % BN:
+    if BM not in GEMM_WAVES_M or BN not in GEMM_WAVES_N:   # ragged M, N: edge tiles store their valid part
         return None
     BK = rl.tile if rl is not None else 64
     while BK > 16 and 2 * (BM + BN) * BK * 2 > LDS_LIMIT:
@@ -396,7 +396,7 @@ void {kname}({params}) {{
   gr_gemm_body<{tpl}>(a, gr_gemm_smem);
 }}
 """
-    grid = (f["M"] // f["BM"]) * (f["N"] // f["BN"])
+    grid = -(-f["M"] // f["BM"]) * -(-f["N"] // f["BN"])
     lds = _gemm_lds(f["BM"], f["BN"], f["BK"])
     return code, {"kernel": kname, "grid": [grid, f["batch"], 1], "block": [nt, 1, 1], "lds": lds,
                   "args": args, "lowering": "gemm",

@@ -129,8 +129,9 @@ int gr_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
  *  Strides are in elements, multiples of 8; batch stride 0 broadcasts.
  *  epilogue: GR_EPI_NONE, GR_EPI_RELU or GR_EPI_SILU, applied to alpha*acc.
  *  (block_m, block_n) in {(128,128), (256,128), (128,256), (256,256)}
- *  (0 = 256); M, N and K must be multiples of the tile (k tile 64 for the
- *  square tiles, 32 otherwise). */
+ *  (0 = 256). Any M; N a multiple of 8; K a multiple of 32 (the square
+ *  tiles use 64-deep k tiles when K allows). Edge tiles of C are stored
+ *  only where valid. */
 #define GR_EPI_NONE 0
 #define GR_EPI_RELU 1
 #define GR_EPI_SILU 2

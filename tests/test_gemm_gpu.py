@@ -52,6 +52,12 @@ CASES = [
     (1, 512, 256, 256, "fp16", "relu", 1.0, True, (256, 256)),
     (1, 256, 256, 128, "bf16", "none", 0.125, True, (128, 256)),
     (3, 128, 256, 64, "fp16", "silu", 1.0, False, (128, 128)),
+    # ragged M / N (edge tiles store only their valid part), K a multiple of 32 only
+    (1, 200, 136, 96, "fp16", "none", 1.0, False, (128, 128)),
+    (1, 300, 1376, 1376, "fp16", "silu", 1.0, False, (256, 256)),
+    (2, 72, 40, 64, "bf16", "relu", 1.0, True, (256, 256)),
+    (1, 1000, 264, 160, "fp16", "none", 0.5, True, (128, 256)),
+    (1, 33, 8, 32, "bf16", "silu", 1.0, False, (256, 128)),
 ]
 
 
@@ -111,7 +117,9 @@ def test_gemm_rejects_bad_shapes():
     a = torch.zeros((200, 64), dtype=torch.float16, device=dev)
     b = torch.zeros((64, 128), dtype=torch.float16, device=dev)
     with pytest.raises(GrError):
-        gemm(a, b, block_m=128, block_n=128)          # M not a tile multiple
+        gemm(a[:, :48], b[:48], block_m=128, block_n=128)   # K not a multiple of 32
+    with pytest.raises(GrError):
+        gemm(a, b[:, :100], block_m=128, block_n=128)       # N not a multiple of 8
     with pytest.raises(GrError):
         gemm(a[:128], b, block_m=64, block_n=64)       # tile not compiled in
     with pytest.raises(ValueError):
@@ -131,6 +139,22 @@ def test_mlp_small_parity(dt):
     torch.cuda.synchronize()
     ref = O.mlp_silu(x.float().numpy(), w1.float().numpy(), w2.float().numpy(), dtype=np.float64)
     _check(y, ref, f"mlp {dt}")
+
+
+def test_mlp_c4_tensor_parallel_shard():
+    """One GPU's share of C4 split eight ways (W1 by columns, W2 by rows:
+    F = 11008 / 8 = 1376, not a multiple of the 256 tile); sampled rows."""
+    dev = _cuda()
+    from grammar.gemm import mlp_fwd
+    from grammar.workloads import C4, mlp_inputs
+    print("[case] mlp C4 shard F=1376", flush=True)
+    x, w1, w2 = mlp_inputs(C4, seed=0)
+    w1s, w2s = w1[:, :1376].contiguous(), w2[:1376].contiguous()
+    y = mlp_fwd(x.to(dev), w1s.to(dev), w2s.to(dev))
+    torch.cuda.synchronize()
+    rows = np.random.default_rng(1).choice(C4.M, 128, replace=False)
+    ref = O.mlp_silu(x[rows].float().numpy(), w1s.float().numpy(), w2s.float().numpy(), dtype=np.float32)
+    _check(y[torch.as_tensor(rows, device=dev)], ref, "mlp C4 shard rows")
 
 
 def test_mlp_c4_sampled_rows():
