@@ -194,6 +194,37 @@ def sdpa_reference(steps: int, seed: int) -> dict:
     return out
 
 
+def shard_shapes(steps: int, seed: int) -> dict:
+    """The kernels at one GPU's share of an 8-way split (not run across GPUs
+    here): C2's 64 heads split by heads (8 per GPU, no exchange), and the C4
+    MLP tensor-parallel (W1 by columns, W2 by rows: F = 11008 / 8 = 1376; the
+    all-reduce of Y is not part of it)."""
+    import torch
+    from grammar.attention import attention_flops, bind_flash_attention
+    from grammar.gemm import mlp_fwd
+    from grammar.workloads import C2, C4, attention_inputs, mlp_inputs
+    out = {}
+    q, k, v = (t[:, :2].contiguous().to("cuda") for t in attention_inputs(C2, seed=seed))
+    flops = attention_flops(C2.B, 2, C2.N, C2.D)
+    for bm, bn in ((256, 128), (128, 128), (64, 64)):
+        launch, _ = bind_flash_attention(q, k, v, block_m=bm, block_n=bn)
+        ms = timed(launch, steps, 10)
+        rec = {"block_m": bm, "block_n": bn, "ms": round(ms, 6), "tflops": round(flops / (ms * 1e-3) / 1e12, 2)}
+        if "C2_8heads" not in out or rec["ms"] < out["C2_8heads"]["ms"]:
+            out["C2_8heads"] = rec
+    log(f"[bench] C2 share (B4 H2, 8 heads): {out['C2_8heads']}")
+    del q, k, v
+    x, w1, w2 = mlp_inputs(C4, seed=seed)
+    x, w1, w2 = x.to("cuda"), w1[:, :1376].contiguous().to("cuda"), w2[:1376].contiguous().to("cuda")
+    h = torch.empty((C4.M, 1376), dtype=x.dtype, device="cuda")
+    y = torch.empty((C4.M, C4.Dm), dtype=x.dtype, device="cuda")
+    ms = timed(lambda: mlp_fwd(x, w1, w2, h=h, out=y), max(5, steps // 10), 3)
+    flops = 2 * 2 * C4.M * C4.Dm * 1376
+    out["C4_tp8_shard"] = {"F": 1376, "ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 2)}
+    log(f"[bench] C4 share (F = 1376): {out['C4_tp8_shard']}")
+    return out
+
+
 def run_descent(cfg, seconds: float, seed: int):
     """The rewrite descent from the naive program for at most `seconds`."""
     import run_attention_search as RS
@@ -226,7 +257,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-mlp", action="store_true")
     ap.add_argument("--no-side", action="store_true",
-                    help="skip the committed descent-found C3 / C4 programs and the torch SDPA reference point")
+                    help="skip the committed descent-found C3 / C4 programs, the torch SDPA reference point "
+                         "and the one-GPU-share shapes")
     ap.add_argument("--block-m", type=int, default=256, help="hand-written kernel: queries per workgroup")
     ap.add_argument("--block-n", type=int, default=128, help="hand-written kernel: keys per tile")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -336,6 +368,7 @@ def main() -> int:
 
     side = None if args.no_side else side_programs(args.steps, args.seed)
     sdpa = None if args.no_side else sdpa_reference(args.steps, args.seed)
+    shards = None if args.no_side else shard_shapes(args.steps, args.seed)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -374,6 +407,7 @@ def main() -> int:
         "mlp_c4": mlp,
         "descent_programs": side,
         "torch_sdpa": sdpa,
+        "one_gpu_share": shards,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

@@ -17,9 +17,11 @@
 //    those registers are then exactly the B operand of the P*V MFMA, and V^T
 //    can be read with one 16-byte LDS load per MFMA.
 //  * Q stays in registers for the whole kernel. K and V tiles are double
-//    buffered in LDS (one barrier per key tile) and prefetched from global
-//    into registers one tile ahead. 16-byte LDS chunks are XOR-swizzled by row
-//    so both the tile writes and the MFMA operand reads are bank-conflict free.
+//    buffered in LDS (one barrier per key tile) and prefetched one tile
+//    ahead: with DIRECT straight from global memory into LDS
+//    (global_load_lds_dwordx4), else through registers. 16-byte LDS chunks
+//    are XOR-swizzled by row so both the tile writes and the MFMA operand
+//    reads are bank-conflict free.
 //  * With TR (the default in every launch path) V, and K when it comes
 //    transposed (KT), are copied into LDS as laid out in memory and the MFMA
 //    fragments are read back with gfx950's transposing LDS read, so no tile is
