@@ -71,6 +71,101 @@ int dispatch_shape(const gr_attn_args& a, int D, bool causal, bool kt, int bm, i
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// Merge of the key-split partials: one thread per (head, query, 8 of D).
+// m_s are the parts' reference maxima (score units), l_s their row sums:
+// O = sum_s w_s O_s / sum_s w_s l_s with w_s = 2^((m_s - max_s m_s) c).
+template <class T, int D>
+__global__ __launch_bounds__(256) void gr_attn_combine_kernel(const float* __restrict__ po, const float* __restrict__ pml,
+                                                              T* o, long long o_sb, long long o_sh, long long o_sn,
+                                                              int B, int H, int Nq, int S, float c) {
+  constexpr int CH = D / 8;
+  const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long rows = (long long)B * H * Nq;
+  if (idx >= rows * CH) return;
+  const int ch = (int)(idx % CH);
+  const long long row = idx / CH;              // (b*H + h) * Nq + q
+  const int q = (int)(row % Nq);
+  const int bh = (int)(row / Nq);
+  const long long stride = rows;               // rows per split
+  float mx = -GR_INF;
+  for (int s = 0; s < S; ++s) mx = fmaxf(mx, pml[(s * stride + row) * 2]);
+  float L = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < S; ++s) {
+    const float* ml = pml + (s * stride + row) * 2;
+    const float w = gr_exp2((ml[0] - mx) * c);
+    L += w * ml[1];
+    const float* src = po + (s * stride + row) * D + ch * 8;
+    const gr_f32x4 v0 = *reinterpret_cast<const gr_f32x4*>(src);
+    const gr_f32x4 v1 = *reinterpret_cast<const gr_f32x4*>(src + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc[e] += w * v0[e];
+      acc[4 + e] += w * v1[e];
+    }
+  }
+  const float inv = 1.0f / L;
+  gr_u32x4 out;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) out[e] = gr_pack2<T>((T)(acc[2 * e] * inv), (T)(acc[2 * e + 1] * inv));
+  const int b = bh / H, h = bh % H;
+  gr_st16(o + b * o_sb + h * o_sh + (long long)q * o_sn + ch * 8, out);
+}
+
+template <class T, int D, int BN, int NW, bool SPLIT>
+void decode_kernel(const gr_attn_args& a, dim3 grid, hipStream_t st) {
+  constexpr int LDS = gr_flash_lds<D, BN>::BYTES;
+  hipLaunchKernelGGL((gr_flash_fwd_kernel<T, D, BN, NW, 1, false, false, false, true, true, SPLIT>), grid,
+                     dim3(NW * 64), LDS, st, a);
+}
+
+template <class T, int D, int BN, bool SPLIT>
+void decode_nw(const gr_attn_args& a, int nw, dim3 grid, hipStream_t st) {
+  if (nw == 1) decode_kernel<T, D, BN, 1, SPLIT>(a, grid, st);
+  else if (nw == 2) decode_kernel<T, D, BN, 2, SPLIT>(a, grid, st);
+  else decode_kernel<T, D, BN, 4, SPLIT>(a, grid, st);
+}
+
+// Decode-shape launch: Nq queries (any count) against N keys, non-causal, K in
+// [B, H, N, D]; 32 queries per wave, up to 4 waves; 64-key tiles (32 when N
+// is not a multiple of 64); S > 1 splits the keys over S workgroups per query
+// tile and merges their partials through the workspace.
+template <class T, int D>
+int launch_decode(gr_attn_args a, int S, void* ws, size_t ws_bytes, hipStream_t st) {
+  const int nw = a.Nq <= 32 ? 1 : a.Nq <= 64 ? 2 : 4;
+  const long long nqt = (a.Nq + 32 * nw - 1) / (32 * nw);
+  const bool bn64 = a.N % 64 == 0;
+  const int bn = bn64 ? 64 : 32;
+  const int tiles = a.N / bn;
+  if (S < 1) S = 1;
+  if (S > tiles) S = tiles;
+  a.kchunk = ((tiles + S - 1) / S) * bn;
+  S = (a.N + a.kchunk - 1) / a.kchunk;         // every part gets keys
+  const long long nblk = (long long)a.B * a.H * nqt;
+  if (nblk > 0x7fffffffLL || S > 65535) return gr::fail(GR_E_ARG, "gr_attn_decode: grid out of range");
+  if (S > 1) {
+    const size_t need = gr_attn_decode_workspace(a.B, a.H, a.Nq, D, S);
+    if (!ws || ws_bytes < need)
+      return gr::fail(GR_E_ARG, "gr_attn_decode: workspace of %zu bytes needed for %d key parts", need, S);
+    a.part_o = static_cast<float*>(ws);
+    a.part_ml = a.part_o + (size_t)S * a.B * a.H * a.Nq * D;
+  }
+  const dim3 grid((unsigned)nblk, (unsigned)S);
+  if (S > 1) {
+    if (bn64) decode_nw<T, D, 64, true>(a, nw, grid, st);
+    else decode_nw<T, D, 32, true>(a, nw, grid, st);
+  } else {
+    if (bn64) decode_nw<T, D, 64, false>(a, nw, grid, st);
+    else decode_nw<T, D, 32, false>(a, nw, grid, st);
+  }
+  int rc = gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_decode launch");
+  if (rc != 0 || S == 1) return rc;
+  const long long threads = (long long)a.B * a.H * a.Nq * (D / 8);
+  hipLaunchKernelGGL((gr_attn_combine_kernel<T, D>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                     a.part_o, a.part_ml, static_cast<T*>(a.o), a.o_sb, a.o_sh, a.o_sn, a.B, a.H, a.Nq, S,
+                     a.scale_log2);
+  return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_decode combine launch");
+}
+
 __global__ void gr_selftest_mfma32_kernel(const _Float16* A, const _Float16* B, float* Dm) {
   const int l = threadIdx.x, l32 = l & 31, g = l >> 5;
   gr_f16x8 a, b;
@@ -113,6 +208,10 @@ extern "C" int gr_attn_fwd(const void* q, const void* k, const void* v, void* o,
   a.B = B;
   a.H = H;
   a.N = N;
+  a.Nq = N;
+  a.kchunk = N;
+  a.part_o = nullptr;
+  a.part_ml = nullptr;
   a.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == GR_F16) return dispatch_shape<_Float16>(a, D, causal != 0, k_transposed != 0, block_m, block_n, st);
@@ -125,4 +224,52 @@ extern "C" int gr_selftest_mfma32(const void* a, const void* b, float* d, void* 
   hipLaunchKernelGGL(gr_selftest_mfma32_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, (const _Float16*)a,
                      (const _Float16*)b, d);
   return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_selftest_mfma32 launch");
+}
+
+extern "C" size_t gr_attn_decode_workspace(int B, int H, int Nq, int D, int splits) {
+  if (B <= 0 || H <= 0 || Nq <= 0 || D <= 0 || splits <= 1) return 0;
+  return (size_t)splits * B * H * Nq * (D + 2) * sizeof(float);
+}
+
+extern "C" int gr_attn_decode(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H, int Nq,
+                              int N, int D, const long long* qs, const long long* ks, const long long* vs,
+                              const long long* os, float scale, int splits, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  if (!q || !k || !v || !o || !qs || !ks || !vs || !os) return gr::fail(GR_E_ARG, "gr_attn_decode: null argument");
+  if (B <= 0 || H <= 0 || Nq <= 0 || N <= 0) return gr::fail(GR_E_ARG, "gr_attn_decode: B, H, Nq, N must be positive");
+  if (N % 32 != 0) return gr::fail(GR_E_ARG, "gr_attn_decode: N=%d keys must be a multiple of 32", N);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || ((uintptr_t)workspace & 15))
+    return gr::fail(GR_E_ARG, "gr_attn_decode: base pointers must be 16-byte aligned");
+  const long long* all[4] = {qs, ks, vs, os};
+  for (int t = 0; t < 4; ++t)
+    for (int i = 0; i < 3; ++i)
+      if (all[t][i] < 0 || (all[t][i] % 8) != 0)
+        return gr::fail(GR_E_ARG, "gr_attn_decode: strides must be non-negative multiples of 8 elements");
+  if (!(scale > 0.f)) return gr::fail(GR_E_ARG, "gr_attn_decode: scale must be positive");
+  gr_attn_args a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.q_sb = qs[0]; a.q_sh = qs[1]; a.q_sn = qs[2];
+  a.k_sb = ks[0]; a.k_sh = ks[1]; a.k_sn = ks[2];
+  a.v_sb = vs[0]; a.v_sh = vs[1]; a.v_sn = vs[2];
+  a.o_sb = os[0]; a.o_sh = os[1]; a.o_sn = os[2];
+  a.B = B;
+  a.H = H;
+  a.N = N;
+  a.Nq = Nq;
+  a.kchunk = N;
+  a.part_o = nullptr;
+  a.part_ml = nullptr;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  hipStream_t st = (hipStream_t)stream;
+#define GR_DT(TT)                                                                        \
+  if (D == 64) return launch_decode<TT, 64>(a, splits, workspace, workspace_bytes, st);  \
+  if (D == 128) return launch_decode<TT, 128>(a, splits, workspace, workspace_bytes, st); \
+  return gr::fail(GR_E_ARG, "gr_attn_decode: head dim D=%d unsupported (64 or 128)", D);
+  if (dtype == GR_F16) { GR_DT(_Float16) }
+  if (dtype == GR_BF16) { GR_DT(__bf16) }
+#undef GR_DT
+  return gr::fail(GR_E_ARG, "gr_attn_decode: dtype %d unsupported (GR_F16 or GR_BF16)", dtype);
 }

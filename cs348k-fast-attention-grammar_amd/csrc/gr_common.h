@@ -81,6 +81,8 @@ __device__ __forceinline__ V gr_as(gr_u32x4 x) { return __builtin_bit_cast(V, x)
 template <class V>
 __device__ __forceinline__ gr_u32x4 gr_raw(V x) { return __builtin_bit_cast(gr_u32x4, x); }
 
+__device__ __forceinline__ int gr_imin(int a, int b) { return a < b ? a : b; }
+
 __device__ __forceinline__ gr_u32x4 gr_ld16(const void* p) {
   return *reinterpret_cast<const gr_u32x4*>(p);
 }

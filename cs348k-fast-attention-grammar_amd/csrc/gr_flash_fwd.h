@@ -30,6 +30,10 @@
 //    whose queries all precede a tile skip its math; the mask is applied only
 //    on diagonal tiles. Heavy query tiles are scheduled first.
 //  * Workgroups of one head are mapped to one XCD so K/V are shared in its L2.
+//  * Nq (queries) may differ from N (keys) for non-causal launches (decode
+//    shapes): query rows past Nq are computed from a copy of the last row and
+//    not stored. SPLIT: the workgroups of a query tile split the keys and
+//    leave partial results that a second kernel merges.
 #pragma once
 #include "gr_common.h"
 
@@ -42,8 +46,15 @@ struct gr_attn_args {
   long long k_sb, k_sh, k_sn;   // for KT layout: k_sn is the stride of the D axis
   long long v_sb, v_sh, v_sn;
   long long o_sb, o_sh, o_sn;
-  int B, H, N;
+  int B, H, N;                  // N: keys
+  int Nq;                       // queries (== N unless a decode-shape launch)
   float scale_log2;             // softmax scale * log2(e)
+  // key-split launches (SPLIT): blockIdx.y = s takes keys [s*kchunk, (s+1)*kchunk)
+  // and writes its unnormalised partial O [s][b*H+h][q][D] and (m, l)
+  // [s][b*H+h][q] in fp32 for gr_attn_combine_kernel
+  int kchunk;
+  float* part_o;
+  float* part_ml;
 };
 
 // The online softmax moves its exponent base only when a row's max grows by
@@ -281,7 +292,7 @@ __device__ __forceinline__ void gr_flash_qk(gr_f32x16 (&s)[BN / 32][QB], const c
 }
 
 template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT, bool PIPE, bool TR = false,
-          bool DIRECT = false>
+          bool DIRECT = false, bool SPLIT = false>
 __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* lds) {
   typedef gr_mfma<T> MF;
   typedef typename MF::vec8 vec8;
@@ -293,19 +304,24 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
   constexpr int DS = D / 16;       // 16-deep contraction steps over D
   typedef gr_flash_lds<D, BN> L;
   static_assert(BN % 32 == 0 && D % 32 == 0, "tile shape");
+  static_assert(!(SPLIT && (CAUSAL || PIPE)), "key split: non-causal, straight schedule");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
-  const int nqt = a.N / BM;
+  const int Nq = a.Nq;
+  const int nqt = (Nq + BM - 1) / BM;
   const int logical = gr_xcd_remap((int)blockIdx.x, (int)gridDim.x);
   const int bh = logical / nqt;
   int qt = logical % nqt;
   if (CAUSAL) qt = nqt - 1 - qt;
   const int b = bh / a.H, h = bh % a.H;
 
+  // this workgroup's keys: all of them, or (SPLIT) part blockIdx.y
+  const int key0 = SPLIT ? (int)blockIdx.y * a.kchunk : 0;
+  const int nkeys = SPLIT ? (a.N - key0 < a.kchunk ? a.N - key0 : a.kchunk) : a.N;
   const T* Qp = (const T*)a.q + b * a.q_sb + h * a.q_sh;
-  const T* Kp = (const T*)a.k + b * a.k_sb + h * a.k_sh;
-  const T* Vp = (const T*)a.v + b * a.v_sb + h * a.v_sh;
+  const T* Kp = (const T*)a.k + b * a.k_sb + h * a.k_sh + key0 * (KT_LAYOUT ? 1LL : a.k_sn);
+  const T* Vp = (const T*)a.v + b * a.v_sb + h * a.v_sh + key0 * a.v_sn;
   T* Op = (T*)a.o + b * a.o_sb + h * a.o_sh;
 
   const int q0 = qt * BM;
@@ -317,7 +333,7 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
   for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds)
-      qf[qb][ds] = gr_as<vec8>(gr_ld16(Qp + (long long)(qw + qb * 32 + l32) * a.q_sn + ds * 16 + 8 * g));
+      qf[qb][ds] = gr_as<vec8>(gr_ld16(Qp + (long long)gr_imin(qw + qb * 32 + l32, Nq - 1) * a.q_sn + ds * 16 + 8 * g));
 
   gr_f32x16 o[DB][QB];
   float m[QB], l[QB];
@@ -352,7 +368,7 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
   const long long k_tile = KT_LAYOUT ? (long long)BN : (long long)BN * a.k_sn;
   const long long v_tile = (long long)BN * a.v_sn;
 
-  const int ntile = CAUSAL ? (q0 + BM + BN - 1) / BN : a.N / BN;
+  const int ntile = CAUSAL ? (q0 + BM + BN - 1) / BN : nkeys / BN;
   const int wq_last = qw + QB * 32 - 1;        // this wave's last query
   auto wave_active = [&](int t) { return !CAUSAL || t * BN <= wq_last; };
 
@@ -515,10 +531,32 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
     }
   }
 
+  if constexpr (SPLIT) {
+    // unnormalised partial O and the (reference max, row sum) it is based on
+    const long long part = (long long)blockIdx.y * a.B * a.H + bh;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int q = qw + qb * 32 + l32;
+      const float lt = l[qb] + gr_xor32(l[qb]);
+      if (q < Nq) {
+        float* po = a.part_o + (part * Nq + q) * D;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const gr_f32x4 w = {o[db][qb][4 * rr], o[db][qb][4 * rr + 1], o[db][qb][4 * rr + 2], o[db][qb][4 * rr + 3]};
+            *reinterpret_cast<gr_f32x4*>(po + db * 32 + 8 * rr + 4 * g) = w;
+          }
+        if (g == 0) *reinterpret_cast<gr_f32x2*>(a.part_ml + (part * Nq + q) * 2) = (gr_f32x2){m[qb], lt};
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const float lt = l[qb] + gr_xor32(l[qb]);
     const float inv = 1.0f / lt;
+    if (qw + qb * 32 + l32 >= Nq) continue;
     T* orow = Op + (long long)(qw + qb * 32 + l32) * a.o_sn;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
@@ -551,10 +589,10 @@ struct gr_flash_wpe {
 // Kernel wrapper used by the prebuilt library; the grammar renderer emits its
 // own wrappers with baked-in shapes around the same body.
 template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT, bool PIPE, bool TR = false,
-          bool DIRECT = false>
+          bool DIRECT = false, bool SPLIT = false>
 __global__ __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(gr_flash_wpe<D, BN, NW, QB, KT_LAYOUT, PIPE>::value)))
 void gr_flash_fwd_kernel(gr_attn_args a) {
   extern __shared__ __attribute__((aligned(16))) char gr_lds[];
-  gr_flash_fwd_body<T, D, BN, NW, QB, CAUSAL, KT_LAYOUT, PIPE, TR, DIRECT>(a, gr_lds);
+  gr_flash_fwd_body<T, D, BN, NW, QB, CAUSAL, KT_LAYOUT, PIPE, TR, DIRECT, SPLIT>(a, gr_lds);
 }

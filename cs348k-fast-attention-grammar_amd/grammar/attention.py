@@ -77,6 +77,54 @@ def flash_attention_fwd(q, k, v, *, causal: bool = False, scale: float | None = 
     return out
 
 
+def decode_splits(B: int, H: int, Nq: int, N: int, cu_count: int = 256) -> int:
+    """Key parts per query tile for gr_attn_decode: enough workgroups for
+    two per compute unit, each part keeping at least four 64-key tiles."""
+    nw = 1 if Nq <= 32 else 2 if Nq <= 64 else 4
+    tiles_q = B * H * -(-Nq // (32 * nw))
+    want = -(-2 * cu_count // tiles_q)
+    return max(1, min(want, N // 256 if N >= 256 else 1))
+
+
+def flash_attention_decode(q, k, v, *, scale: float | None = None, splits: int = 0, out=None,
+                           workspace=None, stream=None):
+    """O = softmax(scale * Q K^T) V for Nq queries against N keys (non-causal):
+    q [B, H, Nq, D], k and v [B, H, N, D] (N a multiple of 32), fp16/bf16 on
+    the GPU. splits = 0 picks the key split (decode_splits); the workspace
+    it needs is allocated here unless given."""
+    import torch
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not t.is_cuda:
+            raise ValueError(f"flash_attention_decode: {name} must be a GPU tensor (no CPU path)")
+        if t.dtype != q.dtype or t.dim() != 4 or t.stride(3) != 1:
+            raise ValueError(f"flash_attention_decode: {name} must be 4-D, q's dtype, unit stride on D")
+    B, H, Nq, D = q.shape
+    N = k.shape[2]
+    if tuple(k.shape) != (B, H, N, D) or tuple(v.shape) != (B, H, N, D):
+        raise ValueError(f"flash_attention_decode: k {tuple(k.shape)} / v {tuple(v.shape)} do not match q {tuple(q.shape)}")
+    if out is None:
+        out = torch.empty((B, H, Nq, D), dtype=q.dtype, device=q.device)
+    elif tuple(out.shape) != (B, H, Nq, D) or out.dtype != q.dtype or out.stride(3) != 1:
+        raise ValueError("flash_attention_decode: bad `out` tensor")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    L = rt.lib()
+    if splits <= 0:
+        splits = decode_splits(B, H, Nq, N, rt.device_info(q.device.index or 0)["cu_count"])
+    need = int(L.gr_attn_decode_workspace(B, H, Nq, D, splits))
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    elif need and workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"flash_attention_decode: workspace of {need} bytes needed")
+    rc = L.gr_attn_decode(
+        ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
+        ctypes.c_void_p(out.data_ptr()), rt.dtype_code(q.dtype), B, H, Nq, N, D,
+        _strides3(q), _strides3(k), _strides3(v), _strides3(out), float(scale), int(splits),
+        ctypes.c_void_p(workspace.data_ptr() if need else None), need, rt._stream_ptr(stream))
+    rt.check(rc, "gr_attn_decode")
+    return out
+
+
 def attention_flops(B: int, H: int, N: int, D: int, causal: bool = False) -> int:
     """Algorithmic FLOPs of attention forward: 4*B*H*N^2*D (two GEMMs), halved
     for a causal mask (old/benchmark.py:354-355 defines the 4*B*H*S^2*D count)."""

@@ -237,7 +237,8 @@ void {kname}({params}) {{
   a.k_sb = {N * D}LL; a.k_sh = 0; a.k_sn = {N};
   a.v_sb = {N * D}LL; a.v_sh = 0; a.v_sn = {D};
   a.o_sb = {N * D}LL; a.o_sh = 0; a.o_sn = {D};
-  a.B = {f['lead']}; a.H = 1; a.N = {N};
+  a.B = {f['lead']}; a.H = 1; a.N = {N}; a.Nq = {N};
+  a.kchunk = {N}; a.part_o = nullptr; a.part_ml = nullptr;
   a.scale_log2 = {_flt(f['scale'] * LOG2E)};
   gr_flash_fwd_body<{T}, {D}, {f['BN']}, {f['NW']}, {f['QB']}, {'true' if f['causal'] else 'false'}, true, {pipe}, true, {direct}>(a, gr_flash_smem);
 }}

@@ -116,6 +116,26 @@ int gr_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
                 const long long* v_strides, const long long* o_strides, int k_transposed,
                 int causal, float scale, int block_m, int block_n, void* stream);
 
+/* Decode-shape attention forward: Nq queries (any count, e.g. 1 for a
+ * decode step) against N keys, O = softmax(scale*Q K^T) V, non-causal.
+ * No counterpart in the reference, whose attention takes Nq == N
+ * (run_attention_search.py:34-114); it is the decode-shape item of the
+ * scope's next steps and serves small B*H*Nq, where the query tiles alone
+ * cannot fill the GPU.
+ *  Q, O: [B, H, Nq, D]; K, V: [B, H, N, D]; strides {batch, head, seq} in
+ *  elements (multiples of 8), unit stride along D. N a multiple of 32; D in
+ *  {64, 128}; dtype GR_F16 or GR_BF16.
+ *  splits: workgroups per query tile that share out the keys (clamped to
+ *  the number of 64- or 32-key tiles); with more than one, the partials go
+ *  through `workspace` (device memory of at least
+ *  gr_attn_decode_workspace(B, H, Nq, D, splits) bytes, 16-byte aligned;
+ *  the call then overwrites it) and a second kernel merges them. */
+size_t gr_attn_decode_workspace(int B, int H, int Nq, int D, int splits);
+int gr_attn_decode(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H, int Nq,
+                   int N, int D, const long long* q_strides, const long long* k_strides,
+                   const long long* v_strides, const long long* o_strides, float scale, int splits,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
 /* Batched GEMM with fused epilogue, C[z] = act(alpha * A[z] @ B[z]).
  * Replaces the grammar's matmul stage (a stage whose body is matmul over a
  * contraction axis, optionally followed by mulc and relu/silu:

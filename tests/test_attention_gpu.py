@@ -165,3 +165,72 @@ def test_rejects_bad_shapes():
     with pytest.raises(ValueError):
         from grammar.attention import flash_attention_fwd
         flash_attention_fwd(q.cpu(), q.cpu(), q.cpu())   # no CPU path
+
+
+DECODE = [
+    # B, H, Nq, N, D, dtype, splits (0 = chosen by decode_splits)
+    (2, 3, 1, 256, 64, "fp16", 0),
+    (1, 4, 7, 512, 128, "bf16", 3),
+    (2, 2, 64, 1024, 64, "fp16", 1),
+    (1, 2, 100, 2048, 128, "fp16", 0),
+    (1, 2, 33, 96, 64, "fp16", 2),           # 96 keys: 32-key tiles
+    (4, 16, 1, 8192, 128, "bf16", 0),
+    (4, 2, 1024, 1024, 64, "fp16", 4),       # C2 at 8 heads, keys split four ways
+]
+
+
+@pytest.mark.parametrize("case", DECODE, ids=lambda c: "-".join(map(str, c)))
+def test_decode_parity(case):
+    """Nq queries against N keys (non-causal), with and without the key split,
+    against the oracle on the same rounded inputs."""
+    dev = _cuda()
+    from grammar.attention import flash_attention_decode
+    B, H, Nq, N, D, dt, splits = case
+    print(f"[case] decode {case}", flush=True)
+    g = torch.Generator("cpu").manual_seed(5)
+    tdt = {"fp16": torch.float16, "bf16": torch.bfloat16}[dt]
+    q = torch.randn((B, H, Nq, D), generator=g).to(tdt)
+    k = torch.randn((B, H, N, D), generator=g).to(tdt)
+    v = torch.randn((B, H, N, D), generator=g).to(tdt)
+    o = flash_attention_decode(q.to(dev), k.to(dev), v.to(dev), splits=splits)
+    torch.cuda.synchronize()
+    ref = O.attention(q.float().numpy(), k.float().numpy(), v.float().numpy())
+    _check(o, ref, f"decode {case}")
+
+
+def test_decode_split_matches_unsplit_and_square_path():
+    """The key split only regroups the sum: split and unsplit agree to float
+    rounding, and Nq == N reproduces gr_attn_fwd at the same tiles."""
+    dev = _cuda()
+    from grammar.attention import flash_attention_decode
+    g = torch.Generator("cpu").manual_seed(6)
+    q, k, v = (torch.randn((2, 4, 512, 64), generator=g).half().to(dev) for _ in range(3))
+    one = flash_attention_decode(q, k, v, splits=1)
+    four = flash_attention_decode(q, k, v, splits=4)
+    torch.cuda.synchronize()
+    assert float((one.float() - four.float()).abs().max()) <= 2e-3
+    sq = _run(q, k, v, block_m=128, block_n=64)
+    assert torch.equal(one, sq)
+
+
+def test_decode_rejects_bad_arguments():
+    dev = _cuda()
+    from grammar import runtime as rt
+    from grammar.attention import flash_attention_decode
+    q = torch.zeros(1, 1, 4, 64, dtype=torch.float16, device=dev)
+    k = torch.zeros(1, 1, 100, 64, dtype=torch.float16, device=dev)
+    with pytest.raises(rt.GrError):
+        flash_attention_decode(q, k, k)                  # keys not a multiple of 32
+    k = torch.zeros(1, 1, 1024, 64, dtype=torch.float16, device=dev)
+    small = torch.empty(16, dtype=torch.uint8, device=dev)
+    with pytest.raises(ValueError):
+        flash_attention_decode(q, k, k, splits=4, workspace=small)   # workspace too small
+    # the C-ABI itself refuses it too (4 key parts need 4*4*(64+2)*4 bytes)
+    import ctypes
+    st = (ctypes.c_longlong * 3)(64 * 4, 64 * 4, 64)
+    stk = (ctypes.c_longlong * 3)(64 * 1024, 64 * 1024, 64)
+    o = torch.empty_like(q)
+    assert rt.lib().gr_attn_decode_workspace(1, 1, 4, 64, 4) == 4 * 4 * 66 * 4
+    rc = rt.lib().gr_attn_decode(q.data_ptr(), k.data_ptr(), k.data_ptr(), o.data_ptr(), rt.dtype_code(q.dtype),
+                                 1, 1, 4, 1024, 64, st, stk, stk, st, 0.125, 4, small.data_ptr(), 16, None)
+    assert rc != 0 and "workspace" in rt.last_error()

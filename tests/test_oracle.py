@@ -25,6 +25,17 @@ def test_attention_matches_float64_bruteforce(causal):
     assert np.allclose(got32, ref, rtol=1e-5, atol=1e-5)
 
 
+def test_fewer_queries_than_keys_are_rows_of_the_square_problem():
+    # the decode shape (Nq != N, non-causal) is the same closed form: its rows
+    # equal the square problem's rows for those queries
+    q, k, v = (_rand((2, 3, 11, 5), s) for s in (7, 8, 9))
+    full = O.attention(q, k, v, dtype=np.float64)
+    rows = [0, 4, 10]
+    part = O.attention(q[:, :, rows], k, v, dtype=np.float64)
+    assert part.shape == (2, 3, 3, 5)
+    assert np.allclose(part, full[:, :, rows], rtol=1e-13, atol=1e-13)
+
+
 def test_kt_layout_equals_k_layout():
     q, k, v = (_rand((1, 2, 9, 4), s) for s in (4, 5, 6))
     a = O.attention(q, k, v, dtype=np.float64)
