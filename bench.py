@@ -198,9 +198,9 @@ def shard_shapes(steps: int, seed: int) -> dict:
     """The kernels at one GPU's share of an 8-way split (not run across GPUs
     here): C2's 64 heads split by heads (8 per GPU, no exchange), and the C4
     MLP tensor-parallel (W1 by columns, W2 by rows: F = 11008 / 8 = 1376; the
-    all-reduce of Y is not part of it)."""
+    all-reduce of Y is not part of it); plus a decode step."""
     import torch
-    from grammar.attention import attention_flops, bind_flash_attention
+    from grammar.attention import attention_flops, bind_flash_attention, bind_flash_attention_decode
     from grammar.gemm import mlp_fwd
     from grammar.workloads import C2, C4, attention_inputs, mlp_inputs
     out = {}
@@ -212,8 +212,25 @@ def shard_shapes(steps: int, seed: int) -> dict:
         rec = {"block_m": bm, "block_n": bn, "ms": round(ms, 6), "tflops": round(flops / (ms * 1e-3) / 1e12, 2)}
         if "C2_8heads" not in out or rec["ms"] < out["C2_8heads"]["ms"]:
             out["C2_8heads"] = rec
-    log(f"[bench] C2 share (B4 H2, 8 heads): {out['C2_8heads']}")
-    del q, k, v
+    # the same share through the key-split launch (partials merged by a second kernel)
+    o = torch.empty_like(q)
+    ws = torch.empty(1 << 24, dtype=torch.uint8, device="cuda")
+    ms = timed(bind_flash_attention_decode(q, k, v, out=o, workspace=ws)[0], steps, 10)
+    out["C2_8heads_keysplit"] = {"ms": round(ms, 6), "tflops": round(flops / (ms * 1e-3) / 1e12, 2)}
+    log(f"[bench] C2 share (B4 H2, 8 heads): {out['C2_8heads']}; key split: {out['C2_8heads_keysplit']}")
+    del q, k, v, o
+    # a decode step: one query per head against an 8192-key cache (HBM-bound: K and V read once)
+    g = torch.Generator("cpu").manual_seed(seed)
+    qd = torch.randn((4, 16, 1, 128), generator=g).to(torch.bfloat16).to("cuda")
+    kd = torch.randn((4, 16, 8192, 128), generator=g).to(torch.bfloat16).to("cuda")
+    vd = torch.randn((4, 16, 8192, 128), generator=g).to(torch.bfloat16).to("cuda")
+    od = torch.empty_like(qd)
+    ms = timed(bind_flash_attention_decode(qd, kd, vd, out=od, workspace=ws)[0], steps, 10)
+    nbytes = 2 * kd.numel() * 2
+    out["decode_B4H16_N8192_d128"] = {"ms": round(ms, 6), "GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                      "frac_of_hbm": round(nbytes / (ms * 1e-3) / 8e12, 4)}
+    log(f"[bench] decode B4 H16 Nq1 N8192 d128 bf16: {out['decode_B4H16_N8192_d128']}")
+    del qd, kd, vd, od, ws
     x, w1, w2 = mlp_inputs(C4, seed=seed)
     x, w1, w2 = x.to("cuda"), w1[:, :1376].contiguous().to("cuda"), w2[:1376].contiguous().to("cuda")
     h = torch.empty((C4.M, 1376), dtype=x.dtype, device="cuda")

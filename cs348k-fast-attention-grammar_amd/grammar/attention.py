@@ -86,12 +86,10 @@ def decode_splits(B: int, H: int, Nq: int, N: int, cu_count: int = 256) -> int:
     return max(1, min(want, N // 256 if N >= 256 else 1))
 
 
-def flash_attention_decode(q, k, v, *, scale: float | None = None, splits: int = 0, out=None,
-                           workspace=None, stream=None):
-    """O = softmax(scale * Q K^T) V for Nq queries against N keys (non-causal):
-    q [B, H, Nq, D], k and v [B, H, N, D] (N a multiple of 32), fp16/bf16 on
-    the GPU. splits = 0 picks the key split (decode_splits); the workspace
-    it needs is allocated here unless given."""
+def bind_flash_attention_decode(q, k, v, *, scale: float | None = None, splits: int = 0, out=None,
+                                workspace=None, stream=None):
+    """Validate once and return (launch, out) for gr_attn_decode, arguments
+    pre-packed (as bind_flash_attention); see flash_attention_decode."""
     import torch
     for name, t in (("q", q), ("k", k), ("v", v)):
         if not t.is_cuda:
@@ -116,12 +114,28 @@ def flash_attention_decode(q, k, v, *, scale: float | None = None, splits: int =
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     elif need and workspace.numel() * workspace.element_size() < need:
         raise ValueError(f"flash_attention_decode: workspace of {need} bytes needed")
-    rc = L.gr_attn_decode(
-        ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
-        ctypes.c_void_p(out.data_ptr()), rt.dtype_code(q.dtype), B, H, Nq, N, D,
-        _strides3(q), _strides3(k), _strides3(v), _strides3(out), float(scale), int(splits),
-        ctypes.c_void_p(workspace.data_ptr() if need else None), need, rt._stream_ptr(stream))
-    rt.check(rc, "gr_attn_decode")
+    fn = L.gr_attn_decode
+    args = (ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
+            ctypes.c_void_p(out.data_ptr()), rt.dtype_code(q.dtype), B, H, Nq, N, D,
+            _strides3(q), _strides3(k), _strides3(v), _strides3(out), float(scale), int(splits),
+            ctypes.c_void_p(workspace.data_ptr() if need else None), need, rt._stream_ptr(stream))
+    keep = (q, k, v, out, workspace)
+
+    def launch():
+        rt.check(fn(*args), "gr_attn_decode")
+        return keep[3]
+    return launch, out
+
+
+def flash_attention_decode(q, k, v, *, scale: float | None = None, splits: int = 0, out=None,
+                           workspace=None, stream=None):
+    """O = softmax(scale * Q K^T) V for Nq queries against N keys (non-causal):
+    q [B, H, Nq, D], k and v [B, H, N, D] (N a multiple of 32), fp16/bf16 on
+    the GPU. splits = 0 picks the key split (decode_splits); the workspace
+    it needs is allocated here unless given."""
+    launch, out = bind_flash_attention_decode(q, k, v, scale=scale, splits=splits, out=out,
+                                              workspace=workspace, stream=stream)
+    launch()
     return out
 
 
