@@ -63,6 +63,17 @@ struct gr_attn_args {
 #define GR_RESCALE_LOG2 8.0f
 #endif
 
+// GR_FLASH_OPT (on unless built with -DGR_FLASH_OPT=0; the pipelined and
+// register-transposing variants always take the max pass): after the first
+// key tile P is computed with the current base and no max pass; only when
+// some p overflowed the P type (the row max grew by more than ~16 powers of
+// two in fp16) is the tile redone with the max pass and a rescale. The score
+// MFMAs of a tile then need not all finish before its first exponentials,
+// and ~35 VALU instructions per 128-key tile and wave drop out.
+#ifndef GR_FLASH_OPT
+#define GR_FLASH_OPT 1
+#endif
+
 template <int V> struct gr_ic { static constexpr int value = V; };
 template <bool C, class X, class Y> struct gr_cond { typedef X type; };
 template <class X, class Y> struct gr_cond<false, X, Y> { typedef Y type; };
@@ -438,6 +449,86 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
             }
           }
       }
+#if GR_FLASH_OPT
+      if constexpr (!PIPE && TR) {
+        // P of the whole tile with the current base; the max pass runs only on
+        // the first tile and when some p overflowed (then the base moves to
+        // the true max and P is recomputed).
+        vec8 pt[KB][2][QB];
+        float lt[QB];
+        auto make_p = [&](const float (&nmc)[QB]) {
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) lt[qb] = 0.f;
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+              for (int qb = 0; qb < QB; ++qb) {
+                gr_u32x4 pw;
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                  const float p0 = gr_exp2(fmaf(s[kb][qb][8 * hf + e], c, nmc[qb]));
+                  const float p1 = gr_exp2(fmaf(s[kb][qb][8 * hf + e + 1], c, nmc[qb]));
+                  const vec2 pp = __builtin_convertvector((gr_f32x2){p0, p1}, vec2);
+                  lt[qb] = MF::sum2(pp, lt[qb]);
+                  pw[e >> 1] = __builtin_bit_cast(unsigned int, pp);
+                }
+                pt[kb][hf][qb] = gr_as<vec8>(pw);
+              }
+        };
+        bool fresh = false;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) fresh |= m[qb] == -GR_INF;
+        bool ok = false;
+        if (!gr_any(fresh)) {
+          float nmc[QB];
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) nmc[qb] = -m[qb] * c;
+          make_p(nmc);
+          bool bad = false;
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) bad |= !(lt[qb] <= 3.0e38f);   // an inf (or NaN) p
+          ok = !gr_any(bad);
+        }
+        if (!ok) {
+          float nmc[QB];
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) {
+            float mt = -GR_INF;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][qb][r]);
+            mt = fmaxf(mt, gr_xor32(mt));
+            const float mn = fmaxf(m[qb], mt);
+            if (gr_any(mn > m[qb])) {
+              const float alpha = gr_exp2((m[qb] - mn) * c);   // m = -inf -> 0
+              l[qb] *= alpha;
+#pragma unroll
+              for (int db = 0; db < DB; ++db) o[db][qb] *= alpha;
+              m[qb] = mn;
+            }
+            nmc[qb] = -((m[qb] == -GR_INF) ? 0.f : m[qb]) * c;
+          }
+          make_p(nmc);
+        }
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) l[qb] += lt[qb];
+        const char* vt = vt0 + ODD * L::VT;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+              const vec8 vf = gr_tr_frag<T, D, false>(vt, kb * 32 + 16 * hf, db * 32, l32 + 32 * g);
+#pragma unroll
+              for (int qb = 0; qb < QB; ++qb) o[db][qb] = MF::mma32(vf, pt[kb][hf][qb], o[db][qb]);
+            }
+      } else
+#endif
+      {
       // Running reference max m. The exponent base is only moved (and the
       // accumulators rescaled) when some lane's true max exceeds m by more
       // than 2^GR_RESCALE_LOG2 in p; otherwise p = 2^((s - m) c) may reach
@@ -495,6 +586,7 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
             for (int qb = 0; qb < QB; ++qb) o[db][qb] = MF::mma32(vf, pf[qb], o[db][qb]);
           }
         }
+      }
       if constexpr (PIPE) {
         // Interleave: per 32-key half block, the next tile's K reads and score
         // MFMAs between this tile's exponentials and its P*V MFMAs, so the

@@ -5,6 +5,8 @@ Bar: max-abs <= 2e-2 and mean-abs <= 2e-3 against
 softmax(QK^T/sqrt(d))V computed in fp32 on the CPU from the fp16/bf16-rounded
 inputs. Full-size configs add size-independent properties (finiteness,
 convex hull of V, bitwise layout/stride invariance, determinism)."""
+import math
+
 import numpy as np
 import pytest
 
@@ -234,3 +236,27 @@ def test_decode_rejects_bad_arguments():
     rc = rt.lib().gr_attn_decode(q.data_ptr(), k.data_ptr(), k.data_ptr(), o.data_ptr(), rt.dtype_code(q.dtype),
                                  1, 1, 4, 1024, 64, st, stk, stk, st, 0.125, 4, small.data_ptr(), 16, None)
     assert rc != 0 and "workspace" in rt.last_error()
+
+
+@pytest.mark.parametrize("dt,causal,D", [("fp16", False, 64), ("bf16", True, 128), ("fp16", True, 64)])
+def test_growing_row_max_takes_the_rebase_path(dt, causal, D):
+    """Keys drifting along the queries make each row's max grow tile after
+    tile, past what an fp16 P holds with the first tile's base: the kernel
+    must notice the overflow and redo those tiles with a moved base."""
+    dev = _cuda()
+    g = torch.Generator("cpu").manual_seed(9)
+    B, H, N = 1, 4, 1024
+    tdt = {"fp16": torch.float16, "bf16": torch.bfloat16}[dt]
+    # q has a common component along (1, ..., 1) and the keys climb along it,
+    # so a row's scores grow by about 3 sqrt(D) from the first to the last key
+    q = torch.randn((B, H, N, D), generator=g) + 1.0
+    k = torch.randn((B, H, N, D), generator=g) + 3.0 * (torch.arange(N).float() / N).view(1, 1, N, 1)
+    v = torch.randn((B, H, N, D), generator=g)
+    q, k, v = q.to(tdt), k.to(tdt), v.to(tdt)
+    s = (q.float() @ k.float().transpose(-1, -2)) / math.sqrt(D)
+    grow = s.amax(-1) - s[..., :64].amax(-1)
+    assert float(grow.median()) > 16 * math.log(2), "inputs must force a rebase"
+    ref = O.attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), causal=causal)
+    for bm, bn in ((128, 64), (256, 64)):
+        o = _run(q.to(dev), k.to(dev), v.to(dev), causal=causal, block_m=bm, block_n=bn)
+        _check(o, ref, f"growing max {dt} causal={causal} D={D} {bm}x{bn}")
