@@ -435,20 +435,24 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
     }
     const int k0 = t * BN;
     if (wave_active(t)) {
-      if constexpr (!PIPE) gr_flash_qk<T, D, BN, QB, KTR>(s, ks0 + ODD * L::KS, qf, l32, g);
-      if (CAUSAL && k0 + BN - 1 > qw) {
+      // this tile's scores (with PIPE they were computed in the previous
+      // iteration) and, on the diagonal of a causal block, the mask
+      auto scores = [&]() {
+        if constexpr (!PIPE) gr_flash_qk<T, D, BN, QB, KTR>(s, ks0 + ODD * L::KS, qf, l32, g);
+        if (CAUSAL && k0 + BN - 1 > qw) {
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
+          for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb) {
-            const int query = qw + qb * 32 + l32;
+            for (int qb = 0; qb < QB; ++qb) {
+              const int query = qw + qb * 32 + l32;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int key = k0 + kb * 32 + ((r < 8) ? (8 * g + r) : (16 + 8 * g + r - 8));
-              if (key > query) s[kb][qb][r] = -GR_INF;
+              for (int r = 0; r < 16; ++r) {
+                const int key = k0 + kb * 32 + ((r < 8) ? (8 * g + r) : (16 + 8 * g + r - 8));
+                if (key > query) s[kb][qb][r] = -GR_INF;
+              }
             }
-          }
-      }
+        }
+      };
 #if GR_FLASH_OPT
       if constexpr (!PIPE && TR) {
         // P of the whole tile with the current base; the max pass runs only on
@@ -481,7 +485,12 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) fresh |= m[qb] == -GR_INF;
         bool ok = false;
-        if (!gr_any(fresh)) {
+        if (gr_any(fresh)) {
+          scores();
+        } else {
+          // the scores and their exponentials in one block, so the first
+          // blocks' exponentials can run while the last score MFMAs do
+          scores();
           float nmc[QB];
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb) nmc[qb] = -m[qb] * c;
@@ -529,6 +538,7 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
       } else
 #endif
       {
+      scores();
       // Running reference max m. The exponent base is only moved (and the
       // accumulators rescaled) when some lane's true max exceeds m by more
       // than 2^GR_RESCALE_LOG2 in p; otherwise p = 2^((s - m) c) may reach
