@@ -288,18 +288,19 @@ __device__ __forceinline__ void gr_flash_qk(gr_f32x16 (&s)[BN / 32][QB], const c
   for (int kb = 0; kb < BN / 32; ++kb)
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) s[kb][qb] = (gr_f32x16)(0.f);
+  // the key blocks' accumulator chains interleaved: consecutive MFMAs are
+  // independent
 #pragma unroll
-  for (int kb = 0; kb < BN / 32; ++kb) {
-    const int row = kb * 32 + l32;
+  for (int ds = 0; ds < D / 16; ++ds)
 #pragma unroll
-    for (int ds = 0; ds < D / 16; ++ds) {
+    for (int kb = 0; kb < BN / 32; ++kb) {
+      const int row = kb * 32 + l32;
       // KTR: K^T tile [D][BN] read transposed; else K rows [BN][D] (rows bit-permuted)
       const vec8 af = KTR ? gr_tr_frag<T, BN, true>(ks, ds * 16, kb * 32, l32 + 32 * g)
                           : gr_as<vec8>(gr_ld16(ks + row * (D * 2) + gr_swz<D / 8>(row, 2 * ds + g) * 16));
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) s[kb][qb] = gr_mfma<T>::mma32(af, qf[qb][ds], s[kb][qb]);
     }
-  }
 }
 
 template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT, bool PIPE, bool TR = false,
