@@ -116,23 +116,27 @@ __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
     for (int j = 0; j < TM; ++j) acc[i][j] = (gr_f32x16)(0.f);
 
   // one k tile of MFMAs from an LDS stage
+  // one k tile of MFMAs from an LDS stage
+  auto frags = [&](const char* cur, int ks, vec8 (&bt)[TN], vec8 (&am)[TM]) {
+#pragma unroll
+    for (int i = 0; i < TN; ++i) {
+      const int row = wn * G::WN + i * 32 + l32;
+      if constexpr (B_KMAJOR)
+        bt[i] = gr_as<vec8>(gr_ld16(cur + G::A_BYTES + row * (BK * 2) + gr_swz<CPR>(row, 2 * ks + g) * 16));
+      else
+        bt[i] = gr_tr_frag<T, BN, false>(cur + G::A_BYTES, ks * 16, wn * G::WN + i * 32, lane);
+    }
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+      const int row = wm * G::WM + j * 32 + l32;
+      am[j] = gr_as<vec8>(gr_ld16(cur + row * (BK * 2) + gr_swz<CPR>(row, 2 * ks + g) * 16));
+    }
+  };
   auto mma_tile = [&](const char* cur) {
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       vec8 bt[TN], am[TM];
-#pragma unroll
-      for (int i = 0; i < TN; ++i) {
-        const int row = wn * G::WN + i * 32 + l32;
-        if constexpr (B_KMAJOR)
-          bt[i] = gr_as<vec8>(gr_ld16(cur + G::A_BYTES + row * (BK * 2) + gr_swz<CPR>(row, 2 * ks + g) * 16));
-        else
-          bt[i] = gr_tr_frag<T, BN, false>(cur + G::A_BYTES, ks * 16, wn * G::WN + i * 32, lane);
-      }
-#pragma unroll
-      for (int j = 0; j < TM; ++j) {
-        const int row = wm * G::WM + j * 32 + l32;
-        am[j] = gr_as<vec8>(gr_ld16(cur + row * (BK * 2) + gr_swz<CPR>(row, 2 * ks + g) * 16));
-      }
+      frags(cur, ks, bt, am);
 #pragma unroll
       for (int i = 0; i < TN; ++i)
 #pragma unroll

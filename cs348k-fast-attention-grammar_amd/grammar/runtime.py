@@ -146,6 +146,11 @@ def compile_source(src: str, name: str = "gr_module.hip", options: list[str] | N
         L.gr_free_code(code)
 
 
+class Kernel(ctypes.c_void_p):
+    """A kernel handle; it holds a reference to its Module, so the code object
+    stays loaded as long as the handle (or a Plan using it) is alive."""
+
+
 class Module:
     """A loaded code object; kernels are looked up by extern "C" name."""
 
@@ -156,11 +161,14 @@ class Module:
         self.handle = h
         self._kernels: dict[str, ctypes.c_void_p] = {}
 
-    def kernel(self, name: str) -> ctypes.c_void_p:
+    def kernel(self, name: str) -> Kernel:
         k = self._kernels.get(name)
         if k is None:
-            k = ctypes.c_void_p()
+            if not self.handle:
+                raise GrError(GR_E_ARG, "Module.kernel: module is closed")
+            k = Kernel()
             check(lib().gr_get_kernel(self.handle, name.encode(), ctypes.byref(k)), f"gr_get_kernel({name})")
+            k.module = self
             self._kernels[name] = k
         return k
 
@@ -192,6 +200,7 @@ class Plan:
         h = ctypes.c_void_p()
         check(lib().gr_plan_create(len(steps), ctypes.byref(h)), "gr_plan_create")
         self.handle = h
+        self._kernels = [st[0] for st in steps]   # keep the kernels' modules loaded
         for i, (k, grid, block, lds, args) in enumerate(steps):
             arr = (ctypes.c_uint64 * max(1, len(args)))(*args)
             check(lib().gr_plan_set_step(h, i, k, _u32x3(*grid), _u32x3(*block), int(lds), arr, len(args)),

@@ -250,3 +250,23 @@ def test_row_lowered_softmax_stages(dt, causal, merges):
     mx, mn = O.errors(o.float().cpu().numpy(), ref)
     print(f"[rows] max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)
     assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL
+
+
+def test_kernel_handle_keeps_its_module_loaded():
+    """A kernel looked up on a temporary Module stays launchable: the handle
+    (and a Plan built from it) keeps the code object loaded."""
+    import gc
+    from grammar import runtime as rt
+    dev = _cuda()
+    code = rt.compile_source('extern "C" __global__ void fill(float* x, float v) { x[threadIdx.x] = v; }\n',
+                             "fill.hip")
+    kern = rt.Module(code).kernel("fill")
+    gc.collect()
+    x = torch.zeros(64, device=dev)
+    import struct
+    plan = rt.Plan([(kern, (1, 1, 1), (64, 1, 1), 0, [x.data_ptr(), struct.unpack("<I", struct.pack("<f", 2.5))[0]])])
+    del kern
+    gc.collect()
+    plan.run()
+    torch.cuda.synchronize()
+    assert torch.all(x == 2.5)
