@@ -20,6 +20,8 @@ of P equal 1; O within the per-column [min V, max V] hull; Q = 0 gives the
 column mean of V (prefix mean for causal); N = 1 gives O = V; key/value
 permutation invariance; per-row score shift invariance; staged == fused;
 MLP against a float64 loop GEMM and the closed-form SiLU at known points.
+The backward (attention_backward, attention_lse) is pinned against central
+finite differences of sum(O * dO) and of the log-sum-exp in float64.
 """
 from __future__ import annotations
 
@@ -116,6 +118,47 @@ def attention_staged(q, kt, v, *, scale: float | None = None, causal: bool = Fal
     P = e / sm                                        # P  = e / sm (broadcast)
     O = P @ v                                         # O  = P @ V        [N,d]
     return {"S": S, "Ss": Ss, "mx": mx, "sb": sb, "e": e, "sm": sm, "P": P, "O": O}
+
+
+def attention_lse(q, k, *, causal: bool = False, scale: float | None = None, dtype=np.float64) -> np.ndarray:
+    """Row log-sum-exp of the scaled (masked) scores, natural log: the
+    per-query statistic a training forward keeps for the backward pass.
+    (No counterpart in the reference, which has no backward.)"""
+    q = np.asarray(q, dtype=dtype)
+    k = np.asarray(k, dtype=dtype)
+    d, n = q.shape[-1], q.shape[-2]
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    s = (q @ np.swapaxes(k, -1, -2)) * scale
+    if causal:
+        s = np.where(np.triu(np.ones((n, k.shape[-2]), dtype=bool), k=1), -np.inf, s)
+    m = s.max(axis=-1, keepdims=True)
+    return (m + np.log(np.exp(s - m).sum(axis=-1, keepdims=True)))[..., 0]
+
+
+def attention_backward(q, k, v, do, *, causal: bool = False, scale: float | None = None,
+                       dtype=np.float64) -> tuple:
+    """Gradients (dQ, dK, dV) of sum(O * dO) for O = softmax(scale Q K^T
+    [causal]) V, from the closed form: P = softmax(S), dV = P^T dO,
+    dP = dO V^T, dS = P * (dP - rowsum(dP * P)), dQ = scale dS K,
+    dK = scale dS^T Q. rowsum(dP * P) equals rowsum(dO * O). (No
+    counterpart in the reference, which has no backward.)"""
+    q, k, v, do = (np.asarray(t, dtype=dtype) for t in (q, k, v, do))
+    d, n = q.shape[-1], q.shape[-2]
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    s = (q @ np.swapaxes(k, -1, -2)) * scale
+    if causal:
+        s = np.where(np.triu(np.ones((n, k.shape[-2]), dtype=bool), k=1), -np.inf, s)
+    p = softmax_rows(s)
+    o = p @ v
+    dv = np.swapaxes(p, -1, -2) @ do
+    dp = do @ np.swapaxes(v, -1, -2)
+    delta = (do * o).sum(axis=-1, keepdims=True)
+    ds = p * (dp - delta)
+    dq = scale * (ds @ k)
+    dk = scale * (np.swapaxes(ds, -1, -2) @ q)
+    return dq, dk, dv
 
 
 def silu(x):

@@ -163,3 +163,39 @@ def test_reference_flop_counts():
     assert 4 * 512 * 512 * 64 + 6 * 512 * 512 == 68681728
     assert C2.flops == 17179869184
     assert C3.flops == 274877906944
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_backward_matches_finite_differences(causal):
+    # d/dx of f = sum(O * dO) by central differences in float64, every element
+    rng = np.random.default_rng(3)
+    q, k, v, do = (rng.standard_normal((2, 5, 4)) for _ in range(4))
+    dq, dk, dv = O.attention_backward(q, k, v, do, causal=causal)
+
+    def f(q_, k_, v_):
+        return float((O.attention(q_, k_, v_, causal=causal, dtype=np.float64) * do).sum())
+    eps = 1e-6
+    for x, g in ((q, dq), (k, dk), (v, dv)):
+        num = np.zeros_like(x)
+        for idx in np.ndindex(*x.shape):
+            xp, xm = x.copy(), x.copy()
+            xp[idx] += eps
+            xm[idx] -= eps
+            args_p = [xp if x is t else t for t in (q, k, v)]
+            args_m = [xm if x is t else t for t in (q, k, v)]
+            num[idx] = (f(*args_p) - f(*args_m)) / (2 * eps)
+        assert np.allclose(g, num, rtol=1e-6, atol=1e-7)
+    if causal:   # the first query attends to one key only: its softmax is constant, its gradient zero
+        assert np.allclose(dq[:, 0], 0.0, atol=1e-12)
+
+
+def test_lse_matches_finite_difference_and_closed_form():
+    rng = np.random.default_rng(4)
+    q, k = rng.standard_normal((3, 6, 4)), rng.standard_normal((3, 6, 4))
+    lse = O.attention_lse(q, k)
+    s = (q @ np.swapaxes(k, -1, -2)) / 2.0
+    assert np.allclose(lse, np.log(np.exp(s).sum(-1)), rtol=1e-13)
+    # softmax rows are exp(s - lse)
+    assert np.allclose(np.exp(s - lse[..., None]), O.softmax_rows(s), rtol=1e-12)
+    lc = O.attention_lse(q, k, causal=True)
+    assert np.allclose(lc[:, 0], s[:, 0, 0])     # the first query sees one key
