@@ -4,7 +4,7 @@
 
 #include <cstdint>
 
-#include "gr_flash_fwd.h"
+#include "gr_flash_bwd.h"
 #include "gr_host.h"
 #include "grammar_rt.h"
 
@@ -183,9 +183,11 @@ __global__ void gr_selftest_mfma32_kernel(const _Float16* A, const _Float16* B, 
 
 }  // namespace
 
-extern "C" int gr_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H, int N,
-                           int D, const long long* qs, const long long* ks, const long long* vs, const long long* os,
-                           int k_transposed, int causal, float scale, int block_m, int block_n, void* stream) {
+namespace {
+
+int attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int dtype, int B, int H, int N, int D,
+             const long long* qs, const long long* ks, const long long* vs, const long long* os, int k_transposed,
+             int causal, float scale, int block_m, int block_n, void* stream) {
   if (!q || !k || !v || !o || !qs || !ks || !vs || !os) return gr::fail(GR_E_ARG, "gr_attn_fwd: null argument");
   if (B <= 0 || H <= 0 || N <= 0) return gr::fail(GR_E_ARG, "gr_attn_fwd: B, H, N must be positive");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
@@ -212,11 +214,105 @@ extern "C" int gr_attn_fwd(const void* q, const void* k, const void* v, void* o,
   a.kchunk = N;
   a.part_o = nullptr;
   a.part_ml = nullptr;
+  a.lse = lse;
   a.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == GR_F16) return dispatch_shape<_Float16>(a, D, causal != 0, k_transposed != 0, block_m, block_n, st);
   if (dtype == GR_BF16) return dispatch_shape<__bf16>(a, D, causal != 0, k_transposed != 0, block_m, block_n, st);
   return gr::fail(GR_E_ARG, "gr_attn_fwd: dtype %d unsupported (GR_F16 or GR_BF16)", dtype);
+}
+
+// Backward tiles: (queries per tile, keys per workgroup) = (64, 128) at D = 64,
+// (32, 64) at D = 128 (one wave per 32 keys).
+template <class T, int D, int BM, int BN>
+int launch_bwd(const gr_attn_bwd_args& a, bool causal, hipStream_t st) {
+  if (a.N % BN != 0 || a.N % BM != 0)
+    return gr::fail(GR_E_ARG, "gr_attn_bwd: N=%d must be a multiple of %d at D=%d", a.N, BN > BM ? BN : BM, D);
+  const long long rows = (long long)a.B * a.H * a.N;
+  hipLaunchKernelGGL((gr_attn_bwd_pre_kernel<T, D>), dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, a);
+  int rc = gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd prologue launch");
+  if (rc) return rc;
+  const dim3 grid((unsigned)((long long)a.B * a.H * (a.N / BN)));
+  constexpr int LDS = gr_attn_bwd_lds<D, BM, BN>::BYTES;
+  if (causal) hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, true>), grid, dim3(BN / 32 * 64), LDS, st, a);
+  else hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, false>), grid, dim3(BN / 32 * 64), LDS, st, a);
+  rc = gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd launch");
+  if (rc) return rc;
+  const long long chunks = rows * (D / 8);
+  hipLaunchKernelGGL((gr_attn_bwd_post_kernel<T, D>), dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, st, a);
+  return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd epilogue launch");
+}
+
+}  // namespace
+
+extern "C" int gr_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H, int N,
+                           int D, const long long* qs, const long long* ks, const long long* vs, const long long* os,
+                           int k_transposed, int causal, float scale, int block_m, int block_n, void* stream) {
+  return attn_fwd(q, k, v, o, nullptr, dtype, B, H, N, D, qs, ks, vs, os, k_transposed, causal, scale, block_m,
+                  block_n, stream);
+}
+
+extern "C" int gr_attn_fwd_train(const void* q, const void* k, const void* v, void* o, float* lse, int dtype, int B,
+                                 int H, int N, int D, const long long* qs, const long long* ks, const long long* vs,
+                                 const long long* os, int k_transposed, int causal, float scale, int block_m,
+                                 int block_n, void* stream) {
+  if (!lse || ((uintptr_t)lse & 3)) return gr::fail(GR_E_ARG, "gr_attn_fwd_train: lse must be a 4-byte aligned buffer");
+  return attn_fwd(q, k, v, o, lse, dtype, B, H, N, D, qs, ks, vs, os, k_transposed, causal, scale, block_m, block_n,
+                  stream);
+}
+
+extern "C" size_t gr_attn_bwd_workspace(int B, int H, int N, int D) {
+  if (B <= 0 || H <= 0 || N <= 0 || D <= 0) return 0;
+  return (size_t)B * H * N * (D + 1) * sizeof(float);
+}
+
+extern "C" int gr_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
+                           const float* lse, void* dq, void* dk, void* dv, int dtype, int B, int H, int N, int D,
+                           const long long* strides, int causal, float scale, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv || !strides)
+    return gr::fail(GR_E_ARG, "gr_attn_bwd: null argument");
+  if (B <= 0 || H <= 0 || N <= 0) return gr::fail(GR_E_ARG, "gr_attn_bwd: B, H, N must be positive");
+  const void* ptrs[10] = {q, k, v, o, dout, dq, dk, dv, workspace, lse};
+  for (int i = 0; i < 9; ++i)
+    if (!aligned16(ptrs[i])) return gr::fail(GR_E_ARG, "gr_attn_bwd: tensors and workspace must be 16-byte aligned");
+  if ((uintptr_t)lse & 3) return gr::fail(GR_E_ARG, "gr_attn_bwd: lse must be 4-byte aligned");
+  for (int i = 0; i < 3; ++i)
+    if (strides[i] < 0 || strides[i] % 8 != 0)
+      return gr::fail(GR_E_ARG, "gr_attn_bwd: strides must be non-negative multiples of 8 elements");
+  if (!(scale > 0.f)) return gr::fail(GR_E_ARG, "gr_attn_bwd: scale must be positive");
+  const size_t need = gr_attn_bwd_workspace(B, H, N, D);
+  if (!workspace || workspace_bytes < need)
+    return gr::fail(GR_E_ARG, "gr_attn_bwd: workspace of %zu bytes needed", need);
+  gr_attn_bwd_args a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.dout = dout;
+  a.lse = lse;
+  a.dq_acc = static_cast<float*>(workspace);
+  a.delta = a.dq_acc + (size_t)B * H * N * D;
+  a.dq = dq;
+  a.dk = dk;
+  a.dv = dv;
+  a.sb = strides[0];
+  a.sh = strides[1];
+  a.sn = strides[2];
+  a.B = B;
+  a.H = H;
+  a.N = N;
+  a.scale = scale;
+  hipStream_t st = (hipStream_t)stream;
+  const bool c = causal != 0;
+#define GR_BWD(TT)                                                               \
+  if (D == 64) return launch_bwd<TT, 64, 64, 128>(a, c, st);                     \
+  if (D == 128) return launch_bwd<TT, 128, 32, 64>(a, c, st);                    \
+  return gr::fail(GR_E_ARG, "gr_attn_bwd: head dim D=%d unsupported (64 or 128)", D);
+  if (dtype == GR_F16) { GR_BWD(_Float16) }
+  if (dtype == GR_BF16) { GR_BWD(__bf16) }
+#undef GR_BWD
+  return gr::fail(GR_E_ARG, "gr_attn_bwd: dtype %d unsupported (GR_F16 or GR_BF16)", dtype);
 }
 
 extern "C" int gr_selftest_mfma32(const void* a, const void* b, float* d, void* stream) {

@@ -52,9 +52,12 @@ struct gr_attn_args {
   // key-split launches (SPLIT): blockIdx.y = s takes keys [s*kchunk, (s+1)*kchunk)
   // and writes its unnormalised partial O [s][b*H+h][q][D] and (m, l)
   // [s][b*H+h][q] in fp32 for gr_attn_combine_kernel
-  int kchunk;
-  float* part_o;
-  float* part_ml;
+  int kchunk = 0;
+  float* part_o = nullptr;
+  float* part_ml = nullptr;
+  // training forward: the row log-sum-exp of the scaled scores (natural log),
+  // [b*H+h][q] fp32, kept for the backward pass; nullptr = not written
+  float* lse = nullptr;
 };
 
 // The online softmax moves its exponent base only when a row's max grows by
@@ -251,7 +254,9 @@ struct gr_tr_loader {
 // column n0 + 16((l/16)%2) + 4c, so that it receives rows k0 + 8(l/32) +
 // 4h + 0..3 of column n0 + perm(l%32), where c = l%4 (PERM: its two bits
 // swapped, i.e. column bits 2 and 3 swapped, as gr_perm32 does to K rows).
-template <class T, int COLS, bool PERM>
+// ROWSWZ: the tile is swizzled with gr_swz (the layout its 16-byte row reads
+// want) instead of gr_swz_tr.
+template <class T, int COLS, bool PERM, bool ROWSWZ = false>
 __device__ __forceinline__ typename gr_mfma<T>::vec8 gr_tr_frag(const char* tile, int k0, int n0, int lane) {
   typedef short v4s __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) v4s lds_v4s;
@@ -262,7 +267,8 @@ __device__ __forceinline__ typename gr_mfma<T>::vec8 gr_tr_frag(const char* tile
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int row = k0 + 8 * (lane >> 5) + 4 * h + ((lane >> 2) & 3);
-    const char* p = tile + row * (COLS * 2) + gr_swz_tr<COLS / 8>(row, col >> 3) * 16 + (col & 7) * 2;
+    const int chunk = ROWSWZ ? gr_swz<COLS / 8>(row, col >> 3) : gr_swz_tr<COLS / 8>(row, col >> 3);
+    const char* p = tile + row * (COLS * 2) + chunk * 16 + (col & 7) * 2;
     const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(__attribute__((address_space(3))) char*)(char*)p);
     const gr_u32x2 w = __builtin_bit_cast(gr_u32x2, v);
     r[2 * h] = w[0];
@@ -660,6 +666,8 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
     const float lt = l[qb] + gr_xor32(l[qb]);
     const float inv = 1.0f / lt;
     if (qw + qb * 32 + l32 >= Nq) continue;
+    // log-sum-exp of scale * s: p = 2^((s - m) c) with c = scale log2(e)
+    if (a.lse && g == 0) a.lse[(long long)bh * Nq + qw + qb * 32 + l32] = (m[qb] * c + __builtin_amdgcn_logf(lt)) * 0.6931471805599453f;
     T* orow = Op + (long long)(qw + qb * 32 + l32) * a.o_sn;
 #pragma unroll
     for (int db = 0; db < DB; ++db)

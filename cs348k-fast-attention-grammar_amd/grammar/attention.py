@@ -77,6 +77,94 @@ def flash_attention_fwd(q, k, v, *, causal: bool = False, scale: float | None = 
     return out
 
 
+def flash_attention_fwd_train(q, k, v, *, causal: bool = False, scale: float | None = None,
+                              block_m: int = 0, block_n: int = 0, out=None, lse=None, stream=None):
+    """flash_attention_fwd that also returns the row log-sum-exp of the scaled
+    scores ([B, H, N] fp32, natural log), kept for flash_attention_bwd.
+    K in [B, H, N, D] layout. Returns (out, lse)."""
+    import torch
+    launch, out = bind_flash_attention(q, k, v, causal=causal, scale=scale, block_m=block_m, block_n=block_n,
+                                       out=out, stream=stream)
+    B, H, N, D = q.shape
+    if lse is None:
+        lse = torch.empty((B, H, N), dtype=torch.float32, device=q.device)
+    elif tuple(lse.shape) != (B, H, N) or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise ValueError("flash_attention_fwd_train: bad `lse` tensor")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    rc = rt.lib().gr_attn_fwd_train(
+        ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
+        ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(lse.data_ptr()), rt.dtype_code(q.dtype), B, H, N, D,
+        _strides3(q), _strides3(k), _strides3(v), _strides3(out), 0, int(bool(causal)), float(scale),
+        int(block_m), int(block_n), rt._stream_ptr(stream))
+    rt.check(rc, "gr_attn_fwd_train")
+    return out, lse
+
+
+def flash_attention_bwd(q, k, v, o, do, lse, *, causal: bool = False, scale: float | None = None,
+                        workspace=None, stream=None):
+    """dQ, dK, dV of sum(O * dO) for the attention forward that produced o and
+    lse (flash_attention_fwd_train). q, k, v, o, do: [B, H, N, D] fp16/bf16
+    on the GPU (made contiguous here: the kernel takes one stride set)."""
+    import torch
+    B, H, N, D = q.shape
+    for name, t in (("k", k), ("v", v), ("o", o), ("do", do)):
+        if tuple(t.shape) != (B, H, N, D) or t.dtype != q.dtype or not t.is_cuda:
+            raise ValueError(f"flash_attention_bwd: {name} must match q ({tuple(q.shape)}, {q.dtype}, GPU)")
+    if tuple(lse.shape) != (B, H, N) or lse.dtype != torch.float32:
+        raise ValueError("flash_attention_bwd: lse must be [B, H, N] float32")
+    q, k, v, o, do, lse = (t.contiguous() for t in (q, k, v, o, do, lse))
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    L = rt.lib()
+    need = int(L.gr_attn_bwd_workspace(B, H, N, D))
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    elif workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"flash_attention_bwd: workspace of {need} bytes needed")
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    rc = L.gr_attn_bwd(
+        ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
+        ctypes.c_void_p(o.data_ptr()), ctypes.c_void_p(do.data_ptr()), ctypes.c_void_p(lse.data_ptr()),
+        ctypes.c_void_p(dq.data_ptr()), ctypes.c_void_p(dk.data_ptr()), ctypes.c_void_p(dv.data_ptr()),
+        rt.dtype_code(q.dtype), B, H, N, D, _strides3(q), int(bool(causal)), float(scale),
+        ctypes.c_void_p(workspace.data_ptr()), need, rt._stream_ptr(stream))
+    rt.check(rc, "gr_attn_bwd")
+    return dq, dk, dv
+
+
+def _autograd_function():
+    import torch
+
+    class FlashAttention(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, q, k, v, causal, scale):
+            q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+            o, lse = flash_attention_fwd_train(q, k, v, causal=causal, scale=scale)
+            ctx.save_for_backward(q, k, v, o, lse)
+            ctx.causal, ctx.scale = causal, scale
+            return o
+
+        @staticmethod
+        def backward(ctx, do):
+            q, k, v, o, lse = ctx.saved_tensors
+            dq, dk, dv = flash_attention_bwd(q, k, v, o, do, lse, causal=ctx.causal, scale=ctx.scale)
+            return dq, dk, dv, None, None
+    return FlashAttention
+
+
+_FLASH_FN = None
+
+
+def flash_attention(q, k, v, *, causal: bool = False, scale: float | None = None):
+    """Differentiable attention on the MI355X kernels: forward through
+    gr_attn_fwd_train, backward through gr_attn_bwd (torch.autograd)."""
+    global _FLASH_FN
+    if _FLASH_FN is None:
+        _FLASH_FN = _autograd_function()
+    return _FLASH_FN.apply(q, k, v, causal, scale)
+
+
 def decode_splits(B: int, H: int, Nq: int, N: int, cu_count: int = 256) -> int:
     """Key parts per query tile for gr_attn_decode: enough workgroups for
     two per compute unit, each part keeping at least four 64-key tiles."""

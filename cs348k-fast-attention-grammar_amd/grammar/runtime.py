@@ -88,6 +88,12 @@ def lib() -> ctypes.CDLL:
         L.gr_gemm.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, _ll2, _ll2, _ll2, i32, i32,
                               ctypes.c_float, i32, i32, vp]
         L.gr_mlp_fwd.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp]
+        L.gr_attn_fwd_train.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, _ll3, _ll3, _ll3, _ll3,
+                                        i32, i32, ctypes.c_float, i32, i32, vp]
+        L.gr_attn_bwd_workspace.argtypes = [i32, i32, i32, i32]
+        L.gr_attn_bwd_workspace.restype = ctypes.c_size_t
+        L.gr_attn_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, _ll3, i32,
+                                  ctypes.c_float, vp, ctypes.c_size_t, vp]
         L.gr_attn_decode_workspace.argtypes = [i32, i32, i32, i32, i32]
         L.gr_attn_decode_workspace.restype = ctypes.c_size_t
         L.gr_attn_decode.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, _ll3, _ll3, _ll3, _ll3,
@@ -102,6 +108,7 @@ EXPORTED = (
     "gr_module_load", "gr_module_free", "gr_get_kernel", "gr_launch", "gr_plan_create",
     "gr_plan_set_step", "gr_plan_run", "gr_plan_free", "gr_plan_time", "gr_attn_fwd",
     "gr_selftest_mfma32", "gr_gemm", "gr_mlp_fwd", "gr_attn_decode_workspace", "gr_attn_decode",
+    "gr_attn_fwd_train", "gr_attn_bwd_workspace", "gr_attn_bwd",
 )
 
 

@@ -116,6 +116,29 @@ int gr_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
                 const long long* v_strides, const long long* o_strides, int k_transposed,
                 int causal, float scale, int block_m, int block_n, void* stream);
 
+/* Training forward: gr_attn_fwd that also writes, per query row, the
+ * log-sum-exp of the scaled (masked) scores, natural log, into lse
+ * [B*H][N] fp32 (4-byte aligned) for gr_attn_bwd. No counterpart in the
+ * reference (forward only); the scope's next-step backward pass. */
+int gr_attn_fwd_train(const void* q, const void* k, const void* v, void* o, float* lse, int dtype, int B,
+                      int H, int N, int D, const long long* q_strides, const long long* k_strides,
+                      const long long* v_strides, const long long* o_strides, int k_transposed, int causal,
+                      float scale, int block_m, int block_n, void* stream);
+
+/* Attention backward: dQ, dK, dV of sum(O * dO) for O = softmax(scale Q K^T
+ * [causal]) V, from Q, K, V, O, dO and the forward's lse. No counterpart in
+ * the reference (forward only); the scope's next-step backward pass.
+ *  All nine [B, H, N, D] tensors share `strides` {batch, head, seq} (in
+ *  elements, multiples of 8; unit stride along D) and are 16-byte aligned.
+ *  D in {64, 128}; N a multiple of 128 (D = 64) or 64 (D = 128).
+ *  workspace: device memory of gr_attn_bwd_workspace(B, H, N, D) bytes,
+ *  16-byte aligned (row statistics and the fp32 dQ accumulator; the call
+ *  overwrites it). */
+size_t gr_attn_bwd_workspace(int B, int H, int N, int D);
+int gr_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, const float* lse,
+                void* dq, void* dk, void* dv, int dtype, int B, int H, int N, int D, const long long* strides,
+                int causal, float scale, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Decode-shape attention forward: Nq queries (any count, e.g. 1 for a
  * decode step) against N keys, O = softmax(scale*Q K^T) V, non-causal.
  * No counterpart in the reference, whose attention takes Nq == N

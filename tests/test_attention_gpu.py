@@ -260,3 +260,61 @@ def test_growing_row_max_takes_the_rebase_path(dt, causal, D):
     for bm, bn in ((128, 64), (256, 64)):
         o = _run(q.to(dev), k.to(dev), v.to(dev), causal=causal, block_m=bm, block_n=bn)
         _check(o, ref, f"growing max {dt} causal={causal} D={D} {bm}x{bn}")
+
+
+BWD = [
+    # B, H, N, D, dtype, causal
+    (1, 2, 256, 64, "fp16", False),
+    (2, 2, 256, 64, "bf16", True),
+    (1, 3, 512, 128, "fp16", True),
+    (1, 2, 256, 128, "bf16", False),
+    (2, 4, 1024, 64, "fp16", True),
+]
+
+
+@pytest.mark.parametrize("case", BWD, ids=lambda c: "-".join(map(str, c)))
+def test_backward_parity(case):
+    """lse of the training forward and dQ, dK, dV of gr_attn_bwd against the
+    float64 oracle (itself pinned by finite differences) on the same rounded
+    inputs. Bar: the attention bar on gradients scaled to unit size
+    (max-abs <= 2e-2 and mean-abs <= 2e-3 of max(1, max|ref|))."""
+    dev = _cuda()
+    from grammar.attention import flash_attention_bwd, flash_attention_fwd_train
+    B, H, N, D, dt, causal = case
+    print(f"[case] backward {case}", flush=True)
+    g = torch.Generator("cpu").manual_seed(13)
+    tdt = {"fp16": torch.float16, "bf16": torch.bfloat16}[dt]
+    q, k, v, do = (torch.randn((B, H, N, D), generator=g).to(tdt) for _ in range(4))
+    o, lse = flash_attention_fwd_train(q.to(dev), k.to(dev), v.to(dev), causal=causal)
+    dq, dk, dv = flash_attention_bwd(q.to(dev), k.to(dev), v.to(dev), o, do.to(dev), lse, causal=causal)
+    torch.cuda.synchronize()
+    qf, kf, vf, dof = (t.double().numpy() for t in (q, k, v, do))
+    ref_lse = O.attention_lse(qf, kf, causal=causal)
+    assert float(np.abs(lse.cpu().numpy() - ref_lse).max()) <= 2e-3, "lse"
+    rdq, rdk, rdv = O.attention_backward(qf, kf, vf, dof, causal=causal)
+    for name, got, ref in (("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+        got = got.float().cpu().numpy()
+        unit = max(1.0, float(np.abs(ref).max()))
+        mx, mn = O.errors(got / unit, ref / unit)
+        print(f"[parity] backward {case} {name}: max-abs {mx:.3e} mean-abs {mn:.3e} (unit {unit:.2f})", flush=True)
+        assert np.isfinite(got).all(), name
+        assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL, (name, mx, mn)
+
+
+def test_autograd_training_step_matches_oracle():
+    """flash_attention as a torch.autograd function: loss.backward() gives the
+    oracle's gradients."""
+    dev = _cuda()
+    from grammar.attention import flash_attention
+    g = torch.Generator("cpu").manual_seed(14)
+    q, k, v = (torch.randn((1, 2, 256, 64), generator=g).half() for _ in range(3))
+    w = torch.randn((1, 2, 256, 64), generator=g).half()
+    qd, kd, vd = (t.to(dev).requires_grad_() for t in (q, k, v))
+    out = flash_attention(qd, kd, vd, causal=True)
+    (out.float() * w.to(dev).float()).sum().backward()
+    torch.cuda.synchronize()
+    rdq, rdk, rdv = O.attention_backward(q.double().numpy(), k.double().numpy(), v.double().numpy(),
+                                         w.double().numpy(), causal=True)
+    for got, ref in ((qd.grad, rdq), (kd.grad, rdk), (vd.grad, rdv)):
+        mx, mn = O.errors(got.float().cpu().numpy(), ref)
+        assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL, (mx, mn)
