@@ -222,25 +222,31 @@ int attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, i
   return gr::fail(GR_E_ARG, "gr_attn_fwd: dtype %d unsupported (GR_F16 or GR_BF16)", dtype);
 }
 
-// Backward tiles: (queries per tile, keys per workgroup) = (64, 128) at D = 64,
-// (32, 64) at D = 128 (one wave per 32 keys).
+// Backward tiles. dK/dV: (queries per tile, keys per workgroup) = (64, 128)
+// at D = 64, (32, 64) at D = 128, one wave per 32 keys. dQ: 4 waves (128
+// queries) per workgroup, key tiles of 64.
 template <class T, int D, int BM, int BN>
 int launch_bwd(const gr_attn_bwd_args& a, bool causal, hipStream_t st) {
-  if (a.N % BN != 0 || a.N % BM != 0)
-    return gr::fail(GR_E_ARG, "gr_attn_bwd: N=%d must be a multiple of %d at D=%d", a.N, BN > BM ? BN : BM, D);
+  constexpr int DQ_NW = 4, DQ_BN = 64;
+  if (a.N % BN != 0 || a.N % BM != 0 || a.N % (DQ_NW * 32) != 0)
+    return gr::fail(GR_E_ARG, "gr_attn_bwd: N=%d must be a multiple of %d at D=%d", a.N, BN > 128 ? BN : 128, D);
   const long long rows = (long long)a.B * a.H * a.N;
   hipLaunchKernelGGL((gr_attn_bwd_pre_kernel<T, D>), dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, a);
   int rc = gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd prologue launch");
   if (rc) return rc;
   const dim3 grid((unsigned)((long long)a.B * a.H * (a.N / BN)));
-  constexpr int LDS = gr_attn_bwd_lds<D, BM, BN>::BYTES;
+  constexpr int LDS = gr_attn_bwd_lds<D, BM>::BYTES;
   if (causal) hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, true>), grid, dim3(BN / 32 * 64), LDS, st, a);
   else hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, false>), grid, dim3(BN / 32 * 64), LDS, st, a);
-  rc = gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd launch");
+  rc = gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd dK/dV launch");
   if (rc) return rc;
-  const long long chunks = rows * (D / 8);
-  hipLaunchKernelGGL((gr_attn_bwd_post_kernel<T, D>), dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, st, a);
-  return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd epilogue launch");
+  const dim3 qgrid((unsigned)((long long)a.B * a.H * (a.N / (DQ_NW * 32))));
+  constexpr int QLDS = gr_attn_bwd_dq_lds<D, DQ_BN>::BYTES;
+  if (causal)
+    hipLaunchKernelGGL((gr_attn_bwd_dq_kernel<T, D, DQ_NW, DQ_BN, true>), qgrid, dim3(DQ_NW * 64), QLDS, st, a);
+  else
+    hipLaunchKernelGGL((gr_attn_bwd_dq_kernel<T, D, DQ_NW, DQ_BN, false>), qgrid, dim3(DQ_NW * 64), QLDS, st, a);
+  return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd dQ launch");
 }
 
 }  // namespace
@@ -263,7 +269,7 @@ extern "C" int gr_attn_fwd_train(const void* q, const void* k, const void* v, vo
 
 extern "C" size_t gr_attn_bwd_workspace(int B, int H, int N, int D) {
   if (B <= 0 || H <= 0 || N <= 0 || D <= 0) return 0;
-  return (size_t)B * H * N * (D + 1) * sizeof(float);
+  return (size_t)B * H * N * sizeof(float);
 }
 
 extern "C" int gr_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
@@ -291,8 +297,7 @@ extern "C" int gr_attn_bwd(const void* q, const void* k, const void* v, const vo
   a.o = o;
   a.dout = dout;
   a.lse = lse;
-  a.dq_acc = static_cast<float*>(workspace);
-  a.delta = a.dq_acc + (size_t)B * H * N * D;
+  a.delta = static_cast<float*>(workspace);
   a.dq = dq;
   a.dk = dk;
   a.dv = dv;

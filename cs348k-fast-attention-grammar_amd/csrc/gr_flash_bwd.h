@@ -5,22 +5,25 @@
 // computes dV = P^T dO, dK = scale dS^T Q, dQ = scale dS K with
 // P = exp(scale Q K^T - L) [causal mask], dS = P * (dO V^T - delta),
 // delta = rowsum(dO * O). Three kernels:
-//  * gr_attn_bwd_pre_kernel: delta per row, and the fp32 dQ accumulator
-//    cleared (a kernel, not a memset, so a captured graph replays it).
-//  * gr_attn_bwd_kernel: one workgroup per block of BN keys of one head,
-//    one wave per 32 of them. K and V of the wave stay in registers as MFMA
-//    operands; dK^T and dV^T accumulate in registers over all query tiles.
-//    Per tile of BM queries (Q and dO double-buffered in LDS, loaded straight
-//    from global memory): S = Q K^T and dP = dO V^T with one key per lane (Q
-//    and dO rows read with bits 2 and 3 of the row index swapped, so each
-//    half-wave's accumulators hold 8 consecutive queries: they are directly
-//    the B operand of dV^T += dO^T P and dK^T += Q^T dS, whose dO^T and Q^T
-//    fragments come from transposing LDS reads of the same tiles). dS^T goes
-//    to LDS and the workgroup forms dQ_tile = dS K from it and a K tile,
-//    added into the fp32 accumulator with hardware float atomics.
-//  * gr_attn_bwd_post_kernel: dQ = scale * accumulator in the storage type.
-// Causal: a key block meets only the query tiles at or after its first key;
-// the mask is applied on the tiles that straddle the diagonal.
+//  * gr_attn_bwd_pre_kernel: delta per row.
+//  * gr_attn_bwd_kernel (dK, dV): one workgroup per block of BN keys of one
+//    head, one wave per 32 of them. K and V of the wave stay in registers as
+//    MFMA operands; dK^T and dV^T accumulate in registers over all query
+//    tiles. Per tile of BM queries (Q and dO double-buffered in LDS, loaded
+//    straight from global memory): S = Q K^T and dP = dO V^T with one key per
+//    lane (Q and dO rows read with bits 2 and 3 of the row index swapped, so
+//    each half-wave's accumulators hold 8 consecutive queries: they are
+//    directly the B operand of dV^T += dO^T P and dK^T += Q^T dS, whose dO^T
+//    and Q^T fragments come from transposing LDS reads of the same tiles).
+//  * gr_attn_bwd_dq_kernel (dQ): the forward's structure -- one wave per 32
+//    queries, Q and dO in registers, K and V tiles streamed through LDS --
+//    recomputing S^T = K Q^T and dP^T = V dO^T with one query per lane, then
+//    dQ^T += K^T dS^T with K^T read transposed from the K tile. Recomputing
+//    the two products costs less here than adding every key block's dQ into
+//    an fp32 accumulator with float atomics (which took over half the time).
+// Causal: a key block meets only the query tiles at or after its first key
+// (and a query tile only the key tiles up to its last query); the mask is
+// applied on the tiles that straddle the diagonal.
 #pragma once
 #include "gr_flash_fwd.h"
 
@@ -32,7 +35,6 @@ struct gr_attn_bwd_args {
   const void* dout;
   const float* lse;     // [b*H+h][N], natural log
   float* delta;         // [b*H+h][N]
-  float* dq_acc;        // [b*H+h][N][D]
   void* dq;
   void* dk;
   void* dv;
@@ -52,7 +54,6 @@ __global__ __launch_bounds__(256) void gr_attn_bwd_pre_kernel(gr_attn_bwd_args a
   const T* o = static_cast<const T*>(a.o) + off;
   const T* dout = static_cast<const T*>(a.dout) + off;
   float acc = 0.f;
-  float* dq = a.dq_acc + row * D;
 #pragma unroll
   for (int c = 0; c < D / 8; ++c) {
     const gr_u32x4 x = gr_ld16(o + 8 * c), y = gr_ld16(dout + 8 * c);
@@ -60,40 +61,15 @@ __global__ __launch_bounds__(256) void gr_attn_bwd_pre_kernel(gr_attn_bwd_args a
     const typename gr_mfma<T>::vec8 yv = gr_as<typename gr_mfma<T>::vec8>(y);
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc += (float)xv[e] * (float)yv[e];
-    *reinterpret_cast<gr_f32x4*>(dq + 8 * c) = (gr_f32x4)(0.f);
-    *reinterpret_cast<gr_f32x4*>(dq + 8 * c + 4) = (gr_f32x4)(0.f);
   }
   a.delta[row] = acc;
 }
 
-template <class T, int D>
-__global__ __launch_bounds__(256) void gr_attn_bwd_post_kernel(gr_attn_bwd_args a) {
-  const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;   // one 8-element chunk
-  const long long chunks = (long long)a.B * a.H * a.N * (D / 8);
-  if (idx >= chunks) return;
-  const long long row = idx / (D / 8);
-  const int c = (int)(idx % (D / 8));
-  const int n = (int)(row % a.N);
-  const int bh = (int)(row / a.N);
-  const float* src = a.dq_acc + row * D + 8 * c;
-  const gr_f32x4 v0 = *reinterpret_cast<const gr_f32x4*>(src);
-  const gr_f32x4 v1 = *reinterpret_cast<const gr_f32x4*>(src + 4);
-  gr_u32x4 w;
-  w[0] = gr_pack2<T>((T)(v0[0] * a.scale), (T)(v0[1] * a.scale));
-  w[1] = gr_pack2<T>((T)(v0[2] * a.scale), (T)(v0[3] * a.scale));
-  w[2] = gr_pack2<T>((T)(v1[0] * a.scale), (T)(v1[1] * a.scale));
-  w[3] = gr_pack2<T>((T)(v1[2] * a.scale), (T)(v1[3] * a.scale));
-  T* dst = static_cast<T*>(a.dq) + (bh / a.H) * a.sb + (bh % a.H) * a.sh + (long long)n * a.sn + 8 * c;
-  gr_st16(dst, w);
-}
-
-template <int D, int BM, int BN>
+template <int D, int BM>
 struct gr_attn_bwd_lds {
   static constexpr int QT = BM * D * 2;          // one Q or dO tile
   static constexpr int STAGE = 2 * QT + 2 * BM * 4;   // Q, dO, then log2-domain L and delta
-  static constexpr int KTILE = BN * D * 2;
-  static constexpr int DST = BN * BM * 2;        // dS^T
-  static constexpr int BYTES = 2 * STAGE + KTILE + DST;
+  static constexpr int BYTES = 2 * STAGE;
 };
 
 template <class T, int D, int BM, int BN, bool CAUSAL>
@@ -103,12 +79,10 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
   typedef typename MF::vec8 vec8;
   constexpr int NW = BN / 32, NT = NW * 64;
   constexpr int DS = D / 16, DB = D / 32, QJ = BM / 32;
-  typedef gr_attn_bwd_lds<D, BM, BN> L;
+  typedef gr_attn_bwd_lds<D, BM> L;
   static_assert(BM % 32 == 0 && BN % 32 == 0 && D % 32 == 0, "tile shape");
   static_assert(2 * BM <= NT, "one thread per statistic of a query tile");
   extern __shared__ __attribute__((aligned(16))) char lds[];
-  char* const k_tile = lds + 2 * L::STAGE;
-  char* const dst_tile = k_tile + L::KTILE;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
@@ -138,9 +112,7 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
     dvt[db] = (gr_f32x16)(0.f);
   }
 
-  gr_lds_loader<T, BN, D, NT, true> kl;     // K tile, read back transposed (dQ)
   gr_lds_loader<T, BM, D, NT> ql;           // Q / dO tiles: row reads and transposing reads
-  kl.init(tid, a.sn);
   ql.init(tid, a.sn);
   const int qt0 = CAUSAL ? key0 / BM : 0;
   const int nqt = a.N / BM;
@@ -153,7 +125,6 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
     if (tid < BM) stat[tid] = a.lse[r0 + tid] * 1.4426950408889634f;
     else if (tid < 2 * BM) stat[tid] = a.delta[r0 + tid - BM];
   };
-  kl.load(K + (long long)key0 * a.sn, k_tile);
   load_tile(qt0, 0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -203,9 +174,6 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
         }
         pb[j][hf] = gr_as<vec8>(pw);
         dsb[j][hf] = gr_as<vec8>(dw);
-        // dS^T row (this lane's key), queries j*32 + 16hf + 8g .. +8: one 16-byte chunk
-        const int krow = wave * 32 + l32;
-        *reinterpret_cast<gr_u32x4*>(dst_tile + krow * (BM * 2) + gr_swz_tr<BM / 8>(krow, 4 * j + 2 * hf + g) * 16) = dw;
       }
       // dV^T += dO^T P and dK^T += Q^T dS over these 32 queries (2 MFMA k-steps)
 #pragma unroll
@@ -217,22 +185,6 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
           dvt[db] = MF::mma32(dot, pb[j][hf], dvt[db]);
           dkt[db] = MF::mma32(qtr, dsb[j][hf], dkt[db]);
         }
-    }
-    __syncthreads();   // dS^T complete
-    // dQ tile (BM x D) = dS K over this block's BN keys; the waves share its 32x32 blocks
-#pragma unroll
-    for (int bi = wave; bi < QJ * DB; bi += NW) {
-      const int qj = bi / DB, db = bi % DB;
-      gr_f32x16 acc = (gr_f32x16)(0.f);
-#pragma unroll
-      for (int ks = 0; ks < BN / 16; ++ks) {
-        const vec8 dsa = gr_tr_frag<T, BM, false>(dst_tile, ks * 16, qj * 32, lane);
-        const vec8 kb_ = gr_tr_frag<T, D, false>(k_tile, ks * 16, db * 32, lane);
-        acc = MF::mma32(dsa, kb_, acc);
-      }
-      float* dq = a.dq_acc + ((long long)bh * a.N + q0 + qj * 32) * D + db * 32 + l32;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) unsafeAtomicAdd(dq + (8 * (r >> 2) + 4 * g + (r & 3)) * D, acc[r]);
     }
     __builtin_amdgcn_s_waitcnt(0);   // the next stage has landed
     __syncthreads();
@@ -253,5 +205,126 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
       wv[1] = gr_pack2<T>((T)dvt[db][4 * rr + 2], (T)dvt[db][4 * rr + 3]);
       *reinterpret_cast<gr_u32x2*>(dk + d) = wk;
       *reinterpret_cast<gr_u32x2*>(dv + d) = wv;
+    }
+}
+
+template <int D, int BN>
+struct gr_attn_bwd_dq_lds {
+  static constexpr int TILE = BN * D * 2;
+  static constexpr int BYTES = 2 * 2 * TILE;   // two stages of K and V
+};
+
+// dQ: one workgroup per NW*32 queries of one head, one wave per 32 (one query
+// per lane); key tiles of BN stream through LDS with their rows stored in the
+// gr_perm32 order, which makes each half-wave's S^T / dP^T accumulators 8
+// consecutive keys -- the B operand of dQ^T += K^T dS^T.
+template <class T, int D, int NW, int BN, bool CAUSAL>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1)))
+void gr_attn_bwd_dq_kernel(gr_attn_bwd_args a) {
+  typedef gr_mfma<T> MF;
+  typedef typename MF::vec8 vec8;
+  constexpr int BM = NW * 32, NT = NW * 64;
+  constexpr int KB = BN / 32, DS = D / 16, DB = D / 32;
+  typedef gr_attn_bwd_dq_lds<D, BN> L;
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int nqt = a.N / BM;
+  const int logical = gr_xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int bh = logical / nqt;
+  int qt = logical % nqt;
+  if (CAUSAL) qt = nqt - 1 - qt;              // the longest query tiles first
+  const long long base = (bh / a.H) * a.sb + (bh % a.H) * a.sh;
+  const T* Q = static_cast<const T*>(a.q) + base;
+  const T* K = static_cast<const T*>(a.k) + base;
+  const T* V = static_cast<const T*>(a.v) + base;
+  const T* dO = static_cast<const T*>(a.dout) + base;
+  const int q0 = qt * BM;
+  const int qw = q0 + wave * 32;
+  const int myq = qw + l32;
+  const float c = a.scale * 1.4426950408889634f;
+
+  vec8 qf[DS], df[DS];
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) {
+    qf[ds] = gr_as<vec8>(gr_ld16(Q + (long long)myq * a.sn + ds * 16 + 8 * g));
+    df[ds] = gr_as<vec8>(gr_ld16(dO + (long long)myq * a.sn + ds * 16 + 8 * g));
+  }
+  const float lse2 = a.lse[(long long)bh * a.N + myq] * 1.4426950408889634f;
+  const float dlt = a.delta[(long long)bh * a.N + myq];
+  gr_f32x16 dqt[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) dqt[db] = (gr_f32x16)(0.f);
+
+  gr_lds_loader<T, BN, D, NT, false, true> kl;   // rows in gr_perm32 order, gr_swz
+  kl.init(tid, a.sn);
+  const int ntile = CAUSAL ? (q0 + BM + BN - 1) / BN : a.N / BN;
+  auto load_tile = [&](int t, int st) {
+    char* s = lds + st * 2 * L::TILE;
+    kl.load(K + (long long)t * BN * a.sn, s);
+    kl.load(V + (long long)t * BN * a.sn, s + L::TILE);
+  };
+  load_tile(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  for (int t = 0; t < ntile; ++t) {
+    const int st = t & 1;
+    if (t + 1 < ntile) load_tile(t + 1, st ^ 1);
+    const char* ks = lds + st * 2 * L::TILE;
+    const char* vs = ks + L::TILE;
+    const int k0 = t * BN;
+    if (!CAUSAL || k0 <= qw + 31) {
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        // S^T and dP^T for keys kb*32.. (LDS rows kb*32 + l32) against this lane's query
+        gr_f32x16 sa = (gr_f32x16)(0.f), dpa = (gr_f32x16)(0.f);
+        const int row = kb * 32 + l32;
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+          const int ch = gr_swz<D / 8>(row, 2 * ds + g);
+          sa = MF::mma32(gr_as<vec8>(gr_ld16(ks + row * (D * 2) + ch * 16)), qf[ds], sa);
+          dpa = MF::mma32(gr_as<vec8>(gr_ld16(vs + row * (D * 2) + ch * 16)), df[ds], dpa);
+        }
+        // register r: key k0 + kb*32 + 8g + r (r < 8) or + 16 + 8g + r - 8
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          gr_u32x4 dw;
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            float d2[2];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              const int r = 8 * hf + e + u;
+              float p = gr_exp2(sa[r] * c - lse2);
+              if (CAUSAL && k0 + kb * 32 + 16 * hf + 8 * g + e + u > myq) p = 0.f;
+              d2[u] = p * (dpa[r] - dlt);
+            }
+            dw[e >> 1] = gr_pack2<T>((T)d2[0], (T)d2[1]);
+          }
+          const vec8 dsb = gr_as<vec8>(dw);
+#pragma unroll
+          for (int db = 0; db < DB; ++db) {
+            const vec8 kt = gr_tr_frag<T, D, false, true, true>(ks, kb * 32 + 16 * hf, db * 32, lane);
+            dqt[db] = MF::mma32(kt, dsb, dqt[db]);
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // the next stage has landed
+    __syncthreads();
+  }
+
+  // dQ = scale dQ^T^T: lane holds query myq, d rows 8(r/4) + 4g + r%4 of block db
+  T* dq = static_cast<T*>(a.dq) + base + (long long)myq * a.sn;
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      gr_u32x2 w;
+      w[0] = gr_pack2<T>((T)(dqt[db][4 * rr] * a.scale), (T)(dqt[db][4 * rr + 1] * a.scale));
+      w[1] = gr_pack2<T>((T)(dqt[db][4 * rr + 2] * a.scale), (T)(dqt[db][4 * rr + 3] * a.scale));
+      *reinterpret_cast<gr_u32x2*>(dq + db * 32 + 8 * rr + 4 * g) = w;
     }
 }

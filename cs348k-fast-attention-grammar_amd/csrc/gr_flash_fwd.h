@@ -255,8 +255,10 @@ struct gr_tr_loader {
 // 4h + 0..3 of column n0 + perm(l%32), where c = l%4 (PERM: its two bits
 // swapped, i.e. column bits 2 and 3 swapped, as gr_perm32 does to K rows).
 // ROWSWZ: the tile is swizzled with gr_swz (the layout its 16-byte row reads
-// want) instead of gr_swz_tr.
-template <class T, int COLS, bool PERM, bool ROWSWZ = false>
+// want) instead of gr_swz_tr. PERMROW: the tile's rows are stored with bits 2
+// and 3 swapped (gr_perm32 within 32-row blocks, k0 a multiple of 16); the
+// lane still receives logical rows k0 + 8(l/32) + 0..7.
+template <class T, int COLS, bool PERM, bool ROWSWZ = false, bool PERMROW = false>
 __device__ __forceinline__ typename gr_mfma<T>::vec8 gr_tr_frag(const char* tile, int k0, int n0, int lane) {
   typedef short v4s __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) v4s lds_v4s;
@@ -266,7 +268,7 @@ __device__ __forceinline__ typename gr_mfma<T>::vec8 gr_tr_frag(const char* tile
   gr_u32x4 r;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const int row = k0 + 8 * (lane >> 5) + 4 * h + ((lane >> 2) & 3);
+    const int row = k0 + (PERMROW ? 4 * (lane >> 5) + 8 * h : 8 * (lane >> 5) + 4 * h) + ((lane >> 2) & 3);
     const int chunk = ROWSWZ ? gr_swz<COLS / 8>(row, col >> 3) : gr_swz_tr<COLS / 8>(row, col >> 3);
     const char* p = tile + row * (COLS * 2) + chunk * 16 + (col & 7) * 2;
     const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(__attribute__((address_space(3))) char*)(char*)p);

@@ -130,10 +130,9 @@ int gr_attn_fwd_train(const void* q, const void* k, const void* v, void* o, floa
  * the reference (forward only); the scope's next-step backward pass.
  *  All nine [B, H, N, D] tensors share `strides` {batch, head, seq} (in
  *  elements, multiples of 8; unit stride along D) and are 16-byte aligned.
- *  D in {64, 128}; N a multiple of 128 (D = 64) or 64 (D = 128).
+ *  D in {64, 128}; N a multiple of 128.
  *  workspace: device memory of gr_attn_bwd_workspace(B, H, N, D) bytes,
- *  16-byte aligned (row statistics and the fp32 dQ accumulator; the call
- *  overwrites it). */
+ *  16-byte aligned (per-row statistics; the call overwrites it). */
 size_t gr_attn_bwd_workspace(int B, int H, int N, int D);
 int gr_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout, const float* lse,
                 void* dq, void* dk, void* dv, int dtype, int B, int H, int N, int D, const long long* strides,
