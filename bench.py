@@ -18,8 +18,10 @@ config C2), with the descent's evals/min measured in the same run.
    after a device synchronize on both sides.
 3. Beside it: the hand-written gr_attn_fwd at its default tile, the C4 MLP
    block through the two-GEMM gr_mlp_fwd, the committed descent-found programs
-   for C3 (causal attention) and C4 (MLP), and the CPU baseline (the staged
-   naive attention in fp32 torch on this host's cores, same seeded inputs).
+   for C3 (causal attention) and C4 (MLP), the training path (forward with
+   row log-sum-exp, then dQ/dK/dV) at C2 and C3 beside torch SDPA, and the
+   CPU baseline (the staged naive attention in fp32 torch on this host's
+   cores, same seeded inputs).
 
 Prints ONE JSON line on stdout; diagnostics go to stderr.
 """
@@ -194,6 +196,69 @@ def sdpa_reference(steps: int, seed: int) -> dict:
     return out
 
 
+def attention_training(steps: int, seed: int) -> dict:
+    """The training path at C2 and C3: gr_attn_fwd_train (forward plus row
+    log-sum-exp) and gr_attn_bwd (dQ, dK, dV), each timed on its own, with
+    torch SDPA's fused backward beside it. Backward FLOPs are 2.5x the forward
+    ones (five N x N x D products instead of two). Gradients of two heads are
+    checked against an fp32 restatement on the GPU, scaled to unit size."""
+    import torch
+    from grammar.attention import bind_flash_attention_bwd, bind_flash_attention_train
+    from grammar.workloads import CONFIGS, attention_inputs
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    out = {}
+    for name in ("C2", "C3"):
+        cfg = CONFIGS[name]
+        q, k, v = (t.to("cuda") for t in attention_inputs(cfg, seed=seed))
+        do = torch.randn(q.shape, generator=torch.Generator("cpu").manual_seed(seed + 1)).to(q.dtype).to("cuda")
+        fwd, o, lse = bind_flash_attention_train(q, k, v, causal=cfg.causal)
+        fwd()
+        bwd, (dq, dk, dv) = bind_flash_attention_bwd(q, k, v, o, do, lse, causal=cfg.causal)
+        n = max(5, steps // (4 if name == "C2" else 20))
+        fwd_ms = timed(fwd, n, 3)
+        bwd_ms = timed(bwd, n, 3)
+        bflops = 2.5 * cfg.flops
+        errs = {}
+        for b, h in ((0, 0), (cfg.B - 1, cfg.H - 1)):
+            qh, kh, vh, doh = (t[b, h].float() for t in (q, k, v, do))
+            s = (qh @ kh.t()) / math.sqrt(cfg.D)
+            if cfg.causal:
+                s = s.masked_fill(torch.ones_like(s, dtype=torch.bool).triu(1), float("-inf"))
+            p = torch.softmax(s, -1)
+            dp = doh @ vh.t()
+            ds = p * (dp - (dp * p).sum(-1, keepdim=True)) / math.sqrt(cfg.D)
+            for gname, got, ref in (("dq", dq, ds @ kh), ("dk", dk, ds.t() @ qh), ("dv", dv, p.t() @ doh)):
+                unit = max(1.0, float(ref.abs().max()))
+                d = (got[b, h].float() - ref).abs() / unit
+                mx, mn = float(d.max()), float(d.mean())
+                prev = errs.get(gname, (0.0, 0.0))
+                errs[gname] = (max(prev[0], mx), max(prev[1], mn))
+        rec = {"fwd_train_ms": round(fwd_ms, 5), "fwd_train_tflops": round(cfg.flops / (fwd_ms * 1e-3) / 1e12, 2),
+               "bwd_ms": round(bwd_ms, 5), "bwd_tflops": round(bflops / (bwd_ms * 1e-3) / 1e12, 2),
+               "check": {g: {"max_abs": round(e[0], 6), "mean_abs": round(e[1], 7)} for g, e in errs.items()},
+               "check_pass": all(e[0] <= 2e-2 and e[1] <= 2e-3 for e in errs.values())}
+        best = None
+        for be in (SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION):
+            try:
+                qr, kr, vr = (t.detach().clone().requires_grad_() for t in (q, k, v))
+                with sdpa_kernel([be]):
+                    ref_o = torch.nn.functional.scaled_dot_product_attention(qr, kr, vr, is_causal=cfg.causal)
+                    ms = timed(lambda: torch.autograd.grad(ref_o, (qr, kr, vr), do, retain_graph=True), n, 3)
+            except RuntimeError as e:   # backend not built for this shape / dtype
+                log(f"[bench] sdpa backward {name} {be.name}: unavailable ({str(e)[:80]})")
+                continue
+            if best is None or ms < best["ms"]:
+                best = {"backend": be.name, "ms": round(ms, 5), "tflops": round(bflops / (ms * 1e-3) / 1e12, 2)}
+            del qr, kr, vr, ref_o
+        rec["torch_sdpa_bwd"] = best
+        out[name] = rec
+        log(f"[bench] {name} training: fwd+lse {fwd_ms:.4f} ms ({rec['fwd_train_tflops']} TFLOP/s), backward "
+            f"{bwd_ms:.4f} ms ({rec['bwd_tflops']} TFLOP/s), check {rec['check_pass']}; torch SDPA backward {best}")
+        del q, k, v, do, o, lse, fwd, bwd, dq, dk, dv
+        torch.cuda.empty_cache()
+    return out
+
+
 def shard_shapes(steps: int, seed: int) -> dict:
     """The kernels at one GPU's share of an 8-way split (not run across GPUs
     here): C2's 64 heads split by heads (8 per GPU, no exchange), and the C4
@@ -274,8 +339,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-mlp", action="store_true")
     ap.add_argument("--no-side", action="store_true",
-                    help="skip the committed descent-found C3 / C4 programs, the torch SDPA reference point "
-                         "and the one-GPU-share shapes")
+                    help="skip the committed descent-found C3 / C4 programs, the torch SDPA reference point, "
+                         "the training (forward + backward) timings and the one-GPU-share shapes")
     ap.add_argument("--block-m", type=int, default=256, help="hand-written kernel: queries per workgroup")
     ap.add_argument("--block-n", type=int, default=128, help="hand-written kernel: keys per tile")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -385,6 +450,7 @@ def main() -> int:
 
     side = None if args.no_side else side_programs(args.steps, args.seed)
     sdpa = None if args.no_side else sdpa_reference(args.steps, args.seed)
+    training = None if args.no_side else attention_training(args.steps, args.seed)
     shards = None if args.no_side else shard_shapes(args.steps, args.seed)
 
     cpu = None
@@ -424,6 +490,7 @@ def main() -> int:
         "mlp_c4": mlp,
         "descent_programs": side,
         "torch_sdpa": sdpa,
+        "training": training,
         "one_gpu_share": shards,
         "cpu_baseline": cpu,
     }

@@ -222,13 +222,21 @@ int attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, i
   return gr::fail(GR_E_ARG, "gr_attn_fwd: dtype %d unsupported (GR_F16 or GR_BF16)", dtype);
 }
 
-// Backward tiles. dK/dV: (queries per tile, keys per workgroup) = (64, 128)
-// at D = 64, (32, 64) at D = 128, one wave per 32 keys. dQ: 4 waves (128
-// queries) per workgroup, key tiles of 64.
+// Backward tiles. dK/dV: (queries per tile, keys per workgroup) = (64, 128),
+// one wave per 32 keys. dQ: key tiles of 64, 8 waves (256 queries) per
+// workgroup when N allows it, else 4.
+template <class T, int D, int NW>
+void launch_bwd_dq(const gr_attn_bwd_args& a, bool causal, hipStream_t st) {
+  constexpr int DQ_BN = 64;
+  const dim3 grid((unsigned)((long long)a.B * a.H * (a.N / (NW * 32))));
+  constexpr int LDS = gr_attn_bwd_dq_lds<D, DQ_BN>::BYTES;
+  if (causal) hipLaunchKernelGGL((gr_attn_bwd_dq_kernel<T, D, NW, DQ_BN, true>), grid, dim3(NW * 64), LDS, st, a);
+  else hipLaunchKernelGGL((gr_attn_bwd_dq_kernel<T, D, NW, DQ_BN, false>), grid, dim3(NW * 64), LDS, st, a);
+}
+
 template <class T, int D, int BM, int BN>
 int launch_bwd(const gr_attn_bwd_args& a, bool causal, hipStream_t st) {
-  constexpr int DQ_NW = 4, DQ_BN = 64;
-  if (a.N % BN != 0 || a.N % BM != 0 || a.N % (DQ_NW * 32) != 0)
+  if (a.N % BN != 0 || a.N % BM != 0 || a.N % 128 != 0)
     return gr::fail(GR_E_ARG, "gr_attn_bwd: N=%d must be a multiple of %d at D=%d", a.N, BN > 128 ? BN : 128, D);
   const long long rows = (long long)a.B * a.H * a.N;
   hipLaunchKernelGGL((gr_attn_bwd_pre_kernel<T, D>), dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, a);
@@ -240,12 +248,8 @@ int launch_bwd(const gr_attn_bwd_args& a, bool causal, hipStream_t st) {
   else hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, false>), grid, dim3(BN / 32 * 64), LDS, st, a);
   rc = gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd dK/dV launch");
   if (rc) return rc;
-  const dim3 qgrid((unsigned)((long long)a.B * a.H * (a.N / (DQ_NW * 32))));
-  constexpr int QLDS = gr_attn_bwd_dq_lds<D, DQ_BN>::BYTES;
-  if (causal)
-    hipLaunchKernelGGL((gr_attn_bwd_dq_kernel<T, D, DQ_NW, DQ_BN, true>), qgrid, dim3(DQ_NW * 64), QLDS, st, a);
-  else
-    hipLaunchKernelGGL((gr_attn_bwd_dq_kernel<T, D, DQ_NW, DQ_BN, false>), qgrid, dim3(DQ_NW * 64), QLDS, st, a);
+  if (a.N % 256 == 0) launch_bwd_dq<T, D, 8>(a, causal, st);
+  else launch_bwd_dq<T, D, 4>(a, causal, st);
   return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd dQ launch");
 }
 
@@ -312,7 +316,7 @@ extern "C" int gr_attn_bwd(const void* q, const void* k, const void* v, const vo
   const bool c = causal != 0;
 #define GR_BWD(TT)                                                               \
   if (D == 64) return launch_bwd<TT, 64, 64, 128>(a, c, st);                     \
-  if (D == 128) return launch_bwd<TT, 128, 32, 64>(a, c, st);                    \
+  if (D == 128) return launch_bwd<TT, 128, 64, 128>(a, c, st);                   \
   return gr::fail(GR_E_ARG, "gr_attn_bwd: head dim D=%d unsupported (64 or 128)", D);
   if (dtype == GR_F16) { GR_BWD(_Float16) }
   if (dtype == GR_BF16) { GR_BWD(__bf16) }

@@ -77,14 +77,14 @@ def flash_attention_fwd(q, k, v, *, causal: bool = False, scale: float | None = 
     return out
 
 
-def flash_attention_fwd_train(q, k, v, *, causal: bool = False, scale: float | None = None,
-                              block_m: int = 0, block_n: int = 0, out=None, lse=None, stream=None):
-    """flash_attention_fwd that also returns the row log-sum-exp of the scaled
-    scores ([B, H, N] fp32, natural log), kept for flash_attention_bwd.
-    K in [B, H, N, D] layout. Returns (out, lse)."""
+def bind_flash_attention_train(q, k, v, *, causal: bool = False, scale: float | None = None,
+                               block_m: int = 0, block_n: int = 0, out=None, lse=None, stream=None):
+    """bind_flash_attention for gr_attn_fwd_train: returns (launch, out, lse),
+    launch() enqueueing the forward that also writes the row log-sum-exp of
+    the scaled scores ([B, H, N] fp32, natural log). K in [B, H, N, D]."""
     import torch
-    launch, out = bind_flash_attention(q, k, v, causal=causal, scale=scale, block_m=block_m, block_n=block_n,
-                                       out=out, stream=stream)
+    _, out = bind_flash_attention(q, k, v, causal=causal, scale=scale, block_m=block_m, block_n=block_n,
+                                  out=out, stream=stream)
     B, H, N, D = q.shape
     if lse is None:
         lse = torch.empty((B, H, N), dtype=torch.float32, device=q.device)
@@ -92,28 +92,46 @@ def flash_attention_fwd_train(q, k, v, *, causal: bool = False, scale: float | N
         raise ValueError("flash_attention_fwd_train: bad `lse` tensor")
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    rc = rt.lib().gr_attn_fwd_train(
-        ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
-        ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(lse.data_ptr()), rt.dtype_code(q.dtype), B, H, N, D,
-        _strides3(q), _strides3(k), _strides3(v), _strides3(out), 0, int(bool(causal)), float(scale),
-        int(block_m), int(block_n), rt._stream_ptr(stream))
-    rt.check(rc, "gr_attn_fwd_train")
+    fn = rt.lib().gr_attn_fwd_train
+    args = (ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
+            ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(lse.data_ptr()), rt.dtype_code(q.dtype), B, H, N, D,
+            _strides3(q), _strides3(k), _strides3(v), _strides3(out), 0, int(bool(causal)), float(scale),
+            int(block_m), int(block_n), rt._stream_ptr(stream))
+    keep = (q, k, v, out, lse)
+
+    def launch():
+        rt.check(fn(*args), "gr_attn_fwd_train")
+        return keep[3], keep[4]
+    return launch, out, lse
+
+
+def flash_attention_fwd_train(q, k, v, *, causal: bool = False, scale: float | None = None,
+                              block_m: int = 0, block_n: int = 0, out=None, lse=None, stream=None):
+    """flash_attention_fwd that also returns the row log-sum-exp of the scaled
+    scores ([B, H, N] fp32, natural log), kept for flash_attention_bwd.
+    K in [B, H, N, D] layout. Returns (out, lse)."""
+    launch, out, lse = bind_flash_attention_train(q, k, v, causal=causal, scale=scale, block_m=block_m,
+                                                  block_n=block_n, out=out, lse=lse, stream=stream)
+    launch()
     return out, lse
 
 
-def flash_attention_bwd(q, k, v, o, do, lse, *, causal: bool = False, scale: float | None = None,
-                        workspace=None, stream=None):
-    """dQ, dK, dV of sum(O * dO) for the attention forward that produced o and
-    lse (flash_attention_fwd_train). q, k, v, o, do: [B, H, N, D] fp16/bf16
-    on the GPU (made contiguous here: the kernel takes one stride set)."""
+def bind_flash_attention_bwd(q, k, v, o, do, lse, *, causal: bool = False, scale: float | None = None,
+                             workspace=None, grads=None, stream=None):
+    """Validate once and return (launch, (dq, dk, dv)): launch() enqueues
+    gr_attn_bwd with pre-packed C arguments. q, k, v, o, do: contiguous
+    [B, H, N, D] fp16/bf16 GPU tensors of one dtype (the kernels take one
+    stride set); lse: [B, H, N] float32 from the training forward; grads: an
+    optional (dq, dk, dv) triple of such tensors to write."""
     import torch
     B, H, N, D = q.shape
-    for name, t in (("k", k), ("v", v), ("o", o), ("do", do)):
+    for name, t in (("q", q), ("k", k), ("v", v), ("o", o), ("do", do)):
         if tuple(t.shape) != (B, H, N, D) or t.dtype != q.dtype or not t.is_cuda:
             raise ValueError(f"flash_attention_bwd: {name} must match q ({tuple(q.shape)}, {q.dtype}, GPU)")
-    if tuple(lse.shape) != (B, H, N) or lse.dtype != torch.float32:
-        raise ValueError("flash_attention_bwd: lse must be [B, H, N] float32")
-    q, k, v, o, do, lse = (t.contiguous() for t in (q, k, v, o, do, lse))
+        if not t.is_contiguous():
+            raise ValueError(f"flash_attention_bwd: {name} must be contiguous")
+    if tuple(lse.shape) != (B, H, N) or lse.dtype != torch.float32 or not lse.is_contiguous():
+        raise ValueError("flash_attention_bwd: lse must be a contiguous [B, H, N] float32 tensor")
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     L = rt.lib()
@@ -122,15 +140,36 @@ def flash_attention_bwd(q, k, v, o, do, lse, *, causal: bool = False, scale: flo
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     elif workspace.numel() * workspace.element_size() < need:
         raise ValueError(f"flash_attention_bwd: workspace of {need} bytes needed")
-    dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
-    rc = L.gr_attn_bwd(
-        ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
-        ctypes.c_void_p(o.data_ptr()), ctypes.c_void_p(do.data_ptr()), ctypes.c_void_p(lse.data_ptr()),
-        ctypes.c_void_p(dq.data_ptr()), ctypes.c_void_p(dk.data_ptr()), ctypes.c_void_p(dv.data_ptr()),
-        rt.dtype_code(q.dtype), B, H, N, D, _strides3(q), int(bool(causal)), float(scale),
-        ctypes.c_void_p(workspace.data_ptr()), need, rt._stream_ptr(stream))
-    rt.check(rc, "gr_attn_bwd")
-    return dq, dk, dv
+    if grads is None:
+        grads = (torch.empty_like(q), torch.empty_like(q), torch.empty_like(q))
+    for t in grads:
+        if tuple(t.shape) != (B, H, N, D) or t.dtype != q.dtype or not t.is_contiguous():
+            raise ValueError("flash_attention_bwd: bad gradient tensor")
+    dq, dk, dv = grads
+    fn = L.gr_attn_bwd
+    args = (ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
+            ctypes.c_void_p(o.data_ptr()), ctypes.c_void_p(do.data_ptr()), ctypes.c_void_p(lse.data_ptr()),
+            ctypes.c_void_p(dq.data_ptr()), ctypes.c_void_p(dk.data_ptr()), ctypes.c_void_p(dv.data_ptr()),
+            rt.dtype_code(q.dtype), B, H, N, D, _strides3(q), int(bool(causal)), float(scale),
+            ctypes.c_void_p(workspace.data_ptr()), need, rt._stream_ptr(stream))
+    keep = (q, k, v, o, do, lse, workspace, grads)
+
+    def launch():
+        rt.check(fn(*args), "gr_attn_bwd")
+        return keep[7]
+    return launch, grads
+
+
+def flash_attention_bwd(q, k, v, o, do, lse, *, causal: bool = False, scale: float | None = None,
+                        workspace=None, stream=None):
+    """dQ, dK, dV of sum(O * dO) for the attention forward that produced o and
+    lse (flash_attention_fwd_train). q, k, v, o, do: [B, H, N, D] fp16/bf16
+    on the GPU (made contiguous here: the kernel takes one stride set)."""
+    q, k, v, o, do, lse = (t.contiguous() for t in (q, k, v, o, do, lse))
+    launch, grads = bind_flash_attention_bwd(q, k, v, o, do, lse, causal=causal, scale=scale,
+                                             workspace=workspace, stream=stream)
+    launch()
+    return grads
 
 
 def _autograd_function():

@@ -269,6 +269,9 @@ BWD = [
     (1, 3, 512, 128, "fp16", True),
     (1, 2, 256, 128, "bf16", False),
     (2, 4, 1024, 64, "fp16", True),
+    (1, 2, 384, 64, "bf16", True),      # N not a multiple of 256: 4-wave dQ workgroups
+    (1, 2, 640, 128, "fp16", False),
+    (1, 2, 2048, 128, "bf16", True),
 ]
 
 
