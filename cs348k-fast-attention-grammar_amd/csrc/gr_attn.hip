@@ -238,19 +238,16 @@ template <class T, int D, int BM, int BN>
 int launch_bwd(const gr_attn_bwd_args& a, bool causal, hipStream_t st) {
   if (a.N % BN != 0 || a.N % BM != 0 || a.N % 128 != 0)
     return gr::fail(GR_E_ARG, "gr_attn_bwd: N=%d must be a multiple of %d at D=%d", a.N, BN > 128 ? BN : 128, D);
-  const long long rows = (long long)a.B * a.H * a.N;
-  hipLaunchKernelGGL((gr_attn_bwd_pre_kernel<T, D>), dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, a);
-  int rc = gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd prologue launch");
+  // dQ first: it also writes delta, which the dK/dV kernel reads
+  if (a.N % 256 == 0) launch_bwd_dq<T, D, 8>(a, causal, st);
+  else launch_bwd_dq<T, D, 4>(a, causal, st);
+  int rc = gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd dQ launch");
   if (rc) return rc;
   const dim3 grid((unsigned)((long long)a.B * a.H * (a.N / BN)));
   constexpr int LDS = gr_attn_bwd_lds<D, BM>::BYTES;
   if (causal) hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, true>), grid, dim3(BN / 32 * 64), LDS, st, a);
   else hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, false>), grid, dim3(BN / 32 * 64), LDS, st, a);
-  rc = gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd dK/dV launch");
-  if (rc) return rc;
-  if (a.N % 256 == 0) launch_bwd_dq<T, D, 8>(a, causal, st);
-  else launch_bwd_dq<T, D, 4>(a, causal, st);
-  return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd dQ launch");
+  return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd dK/dV launch");
 }
 
 }  // namespace

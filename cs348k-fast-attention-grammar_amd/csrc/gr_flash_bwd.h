@@ -5,7 +5,6 @@
 // computes dV = P^T dO, dK = scale dS^T Q, dQ = scale dS K with
 // P = exp(scale Q K^T - L) [causal mask], dS = P * (dO V^T - delta),
 // delta = rowsum(dO * O). Three kernels:
-//  * gr_attn_bwd_pre_kernel: delta per row.
 //  * gr_attn_bwd_kernel (dK, dV): one workgroup per block of BN keys of one
 //    head, one wave per 32 of them. K and V of the wave stay in registers as
 //    MFMA operands; dK^T and dV^T accumulate in registers over all query
@@ -21,6 +20,8 @@
 //    dQ^T += K^T dS^T with K^T read transposed from the K tile. Recomputing
 //    the two products costs less here than adding every key block's dQ into
 //    an fp32 accumulator with float atomics (which took over half the time).
+//    It runs first and also forms delta = rowsum(dO * O) of its queries from
+//    the dO fragments it holds, storing it for the dK/dV kernel.
 // Causal: a key block meets only the query tiles at or after its first key
 // (and a query tile only the key tiles up to its last query); the mask is
 // applied on the tiles that straddle the diagonal.
@@ -34,7 +35,7 @@ struct gr_attn_bwd_args {
   const void* o;
   const void* dout;
   const float* lse;     // [b*H+h][N], natural log
-  float* delta;         // [b*H+h][N]
+  float* delta;         // [b*H+h][N]: rowsum(dO * O), written by the dQ kernel
   void* dq;
   void* dk;
   void* dv;
@@ -42,28 +43,6 @@ struct gr_attn_bwd_args {
   int B, H, N;
   float scale;
 };
-
-template <class T, int D>
-__global__ __launch_bounds__(256) void gr_attn_bwd_pre_kernel(gr_attn_bwd_args a) {
-  const long long row = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  const long long rows = (long long)a.B * a.H * a.N;
-  if (row >= rows) return;
-  const int n = (int)(row % a.N);
-  const int bh = (int)(row / a.N);
-  const long long off = (bh / a.H) * a.sb + (bh % a.H) * a.sh + (long long)n * a.sn;
-  const T* o = static_cast<const T*>(a.o) + off;
-  const T* dout = static_cast<const T*>(a.dout) + off;
-  float acc = 0.f;
-#pragma unroll
-  for (int c = 0; c < D / 8; ++c) {
-    const gr_u32x4 x = gr_ld16(o + 8 * c), y = gr_ld16(dout + 8 * c);
-    const typename gr_mfma<T>::vec8 xv = gr_as<typename gr_mfma<T>::vec8>(x);
-    const typename gr_mfma<T>::vec8 yv = gr_as<typename gr_mfma<T>::vec8>(y);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc += (float)xv[e] * (float)yv[e];
-  }
-  a.delta[row] = acc;
-}
 
 template <int D, int BM>
 struct gr_attn_bwd_lds {
@@ -112,7 +91,7 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
     dvt[db] = (gr_f32x16)(0.f);
   }
 
-  gr_lds_loader<T, BM, D, NT> ql;           // Q / dO tiles: row reads and transposing reads
+  gr_lds_loader<T, BM, D, NT, false, false, true> ql;   // Q / dO tiles: row reads and transposing reads
   ql.init(tid, a.sn);
   const int qt0 = CAUSAL ? key0 / BM : 0;
   const int nqt = a.N / BM;
@@ -147,7 +126,7 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
       const int row = j * 32 + gr_perm32(l32);
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
-        const int ch = gr_swz<D / 8>(row, 2 * ds + g);
+        const int ch = gr_swz_rt<D / 8>(row, 2 * ds + g);
         const vec8 qa = gr_as<vec8>(gr_ld16(qs + row * (D * 2) + ch * 16));
         const vec8 da = gr_as<vec8>(gr_ld16(dos + row * (D * 2) + ch * 16));
         sa = MF::mma32(qa, kf[ds], sa);
@@ -252,12 +231,25 @@ void gr_attn_bwd_dq_kernel(gr_attn_bwd_args a) {
     df[ds] = gr_as<vec8>(gr_ld16(dO + (long long)myq * a.sn + ds * 16 + 8 * g));
   }
   const float lse2 = a.lse[(long long)bh * a.N + myq] * 1.4426950408889634f;
-  const float dlt = a.delta[(long long)bh * a.N + myq];
+  // delta of this lane's query: its half of the row (d = ds*16 + 8g + e), then
+  // the other half from lane ^ 32
+  float dlt = 0.f;
+  {
+    const T* O = static_cast<const T*>(a.o) + base + (long long)myq * a.sn;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      const vec8 ov = gr_as<vec8>(gr_ld16(O + ds * 16 + 8 * g));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dlt = fmaf((float)ov[e], (float)df[ds][e], dlt);
+    }
+    dlt += gr_xor32(dlt);
+    if (g == 0) a.delta[(long long)bh * a.N + myq] = dlt;
+  }
   gr_f32x16 dqt[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) dqt[db] = (gr_f32x16)(0.f);
 
-  gr_lds_loader<T, BN, D, NT, false, true> kl;   // rows in gr_perm32 order, gr_swz
+  gr_lds_loader<T, BN, D, NT, false, true, true> kl;   // rows in gr_perm32 order, gr_swz_rt
   kl.init(tid, a.sn);
   const int ntile = CAUSAL ? (q0 + BM + BN - 1) / BN : a.N / BN;
   auto load_tile = [&](int t, int st) {
@@ -283,7 +275,7 @@ void gr_attn_bwd_dq_kernel(gr_attn_bwd_args a) {
         const int row = kb * 32 + l32;
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
-          const int ch = gr_swz<D / 8>(row, 2 * ds + g);
+          const int ch = gr_swz_rt<D / 8>(row, 2 * ds + g);
           sa = MF::mma32(gr_as<vec8>(gr_ld16(ks + row * (D * 2) + ch * 16)), qf[ds], sa);
           dpa = MF::mma32(gr_as<vec8>(gr_ld16(vs + row * (D * 2) + ch * 16)), df[ds], dpa);
         }

@@ -113,6 +113,20 @@ __device__ __forceinline__ int gr_swz_tr(int row, int chunk) {
   else return chunk;
 }
 
+// Swizzle of tiles read both ways: by 16-byte row reads (16 consecutive rows,
+// one chunk) and by gr_tr_frag (4 consecutive rows x 4 consecutive chunks per
+// 32 lanes). With 64 four-byte banks both touch 16 distinct 16-byte bank
+// groups: h(row) is a bijection of the row's low four bits (bits 1-3 at
+// 128-byte rows, where bit 0 already selects the half of the banks), and its
+// top two bits differ between the four rows of an aligned group (bit 2 for
+// the two rows of equal parity at 128-byte rows).
+template <int CPR>
+__device__ __forceinline__ int gr_swz_rt(int row, int chunk) {
+  if constexpr (CPR >= 16) return chunk ^ (((row & 3) << 2) | ((row >> 2) & 3));     // 256+ B rows
+  else if constexpr (CPR == 8) return chunk ^ ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));  // 128 B rows
+  else return gr_swz<CPR>(row, chunk);
+}
+
 // Global [ROWS][COLS] tile (row stride ld elements) -> LDS rows, same shape.
 // Per-thread global and LDS offsets are computed once (init) and reused for
 // every tile, so the main loop spends no VALU on address arithmetic. TRSWZ
@@ -155,9 +169,10 @@ struct gr_row_loader {
 // at base + 16 l, so the swizzle is applied on the global side: the lane that
 // lands on LDS slot (row, physical chunk) fetches logical chunk swz(row,
 // physical chunk) (the XOR swizzles are involutions); with PERM, LDS row r
-// holds global row gr_perm32(r) (also an involution). The data is in LDS once
-// the wave's vmcnt drains; callers wait on it before the publishing barrier.
-template <class T, int ROWS, int COLS, int NT, bool TRSWZ = false, bool PERM = false>
+// holds global row gr_perm32(r) (also an involution). RTSWZ: gr_swz_rt
+// instead of gr_swz / gr_swz_tr. The data is in LDS once the wave's vmcnt
+// drains; callers wait on it before the publishing barrier.
+template <class T, int ROWS, int COLS, int NT, bool TRSWZ = false, bool PERM = false, bool RTSWZ = false>
 struct gr_lds_loader {
   static constexpr int CPR = COLS / 8;
   static constexpr int CHUNKS = ROWS * CPR;
@@ -173,7 +188,7 @@ struct gr_lds_loader {
     for (int i = 0; i < PER; ++i) {
       const int c = tid + i * NT;
       const int row = c / CPR, pc = c % CPR;
-      const int lc = TRSWZ ? gr_swz_tr<CPR>(row, pc) : gr_swz<CPR>(row, pc);
+      const int lc = RTSWZ ? gr_swz_rt<CPR>(row, pc) : TRSWZ ? gr_swz_tr<CPR>(row, pc) : gr_swz<CPR>(row, pc);
       const int srow = PERM ? gr_perm32(row) : row;
       goff[i] = (int)((srow < rows_valid ? srow : rows_valid - 1) * ld) + (lc < chunks_valid ? lc : chunks_valid - 1) * 8;
     }
@@ -254,11 +269,11 @@ struct gr_tr_loader {
 // column n0 + 16((l/16)%2) + 4c, so that it receives rows k0 + 8(l/32) +
 // 4h + 0..3 of column n0 + perm(l%32), where c = l%4 (PERM: its two bits
 // swapped, i.e. column bits 2 and 3 swapped, as gr_perm32 does to K rows).
-// ROWSWZ: the tile is swizzled with gr_swz (the layout its 16-byte row reads
-// want) instead of gr_swz_tr. PERMROW: the tile's rows are stored with bits 2
+// RTSWZ: the tile is swizzled with gr_swz_rt (a tile that 16-byte row reads
+// use as well) instead of gr_swz_tr. PERMROW: the tile's rows are stored with bits 2
 // and 3 swapped (gr_perm32 within 32-row blocks, k0 a multiple of 16); the
 // lane still receives logical rows k0 + 8(l/32) + 0..7.
-template <class T, int COLS, bool PERM, bool ROWSWZ = false, bool PERMROW = false>
+template <class T, int COLS, bool PERM, bool RTSWZ = false, bool PERMROW = false>
 __device__ __forceinline__ typename gr_mfma<T>::vec8 gr_tr_frag(const char* tile, int k0, int n0, int lane) {
   typedef short v4s __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) v4s lds_v4s;
@@ -269,7 +284,7 @@ __device__ __forceinline__ typename gr_mfma<T>::vec8 gr_tr_frag(const char* tile
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int row = k0 + (PERMROW ? 4 * (lane >> 5) + 8 * h : 8 * (lane >> 5) + 4 * h) + ((lane >> 2) & 3);
-    const int chunk = ROWSWZ ? gr_swz<COLS / 8>(row, col >> 3) : gr_swz_tr<COLS / 8>(row, col >> 3);
+    const int chunk = RTSWZ ? gr_swz_rt<COLS / 8>(row, col >> 3) : gr_swz_tr<COLS / 8>(row, col >> 3);
     const char* p = tile + row * (COLS * 2) + chunk * 16 + (col & 7) * 2;
     const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(__attribute__((address_space(3))) char*)(char*)p);
     const gr_u32x2 w = __builtin_bit_cast(gr_u32x2, v);
