@@ -95,12 +95,19 @@ def measured_traffic(key: str):
         return None
 
 
-def timed(step, steps: int, warmup: int) -> float:
-    """ms per step: warmup, then `steps` calls between two events on the
+def timed(step, steps: int, warmup: int, min_warm_s: float = 0.05) -> float:
+    """ms per step: `warmup` untimed calls (continued until the GPU has been
+    busy for at least min_warm_s: its clocks ramp up over the first tens of
+    milliseconds of load), then `steps` calls between two events on the
     current stream, synchronized on both sides."""
     import torch
-    for _ in range(warmup):
+    t0 = time.perf_counter()
+    n = 0
+    while n < warmup or time.perf_counter() - t0 < min_warm_s:
         step()
+        n += 1
+        if n % 64 == 0 or n == warmup:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
@@ -330,7 +337,9 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=2000,
+                    help="untimed steps before the timed ones (at C2 about 50 ms: the GPU clocks ramp up "
+                         "over the first tens of milliseconds of load)")
     ap.add_argument("--config", default="C2", choices=["C2", "C3"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--kernel", default="descent", choices=["descent", "handwritten"])
@@ -409,8 +418,8 @@ def main() -> int:
         kernel = {"name": "gr_flash_fwd (hand-written)", "block_m": args.block_m, "block_n": args.block_n}
         traffic_key = f"{cfg.name}:{cfg.dtype}:flash:bm{args.block_m}:bn{args.block_n}"
 
-    # 2. the timed region
-    ms = timed(step, args.steps, args.warmup)
+    # 2. the timed region (exactly W warmup steps, then K timed ones)
+    ms = timed(step, args.steps, args.warmup, min_warm_s=0.0)
     tflops = cfg.flops / (ms * 1e-3) / 1e12
     log(f"[bench] {cfg.name} {kernel['name']}: {ms * 1e3:.2f} us/step  {tflops:.1f} TFLOP/s  "
         f"{100 * tflops / peak:.1f}% of peak")

@@ -70,9 +70,11 @@ struct gr_attn_args {
 // register-transposing variants always take the max pass): after the first
 // key tile P is computed with the current base and no max pass; only when
 // some p overflowed the P type (the row max grew by more than ~16 powers of
-// two in fp16) is the tile redone with the max pass and a rescale. The score
-// MFMAs of a tile then need not all finish before its first exponentials,
-// and ~35 VALU instructions per 128-key tile and wave drop out.
+// two in fp16) is the tile redone with the max pass and a rescale. Q is
+// pre-scaled by scale log2(e) and the score MFMAs start from -base, so p is
+// one exp2 of the accumulator. The score MFMAs of a tile then need not all
+// finish before its first exponentials, and ~100 VALU instructions per
+// 128-key tile and wave drop out.
 #ifndef GR_FLASH_OPT
 #define GR_FLASH_OPT 1
 #endif
@@ -80,6 +82,8 @@ struct gr_attn_args {
 template <int V> struct gr_ic { static constexpr int value = V; };
 template <bool C, class X, class Y> struct gr_cond { typedef X type; };
 template <class X, class Y> struct gr_cond<false, X, Y> { typedef Y type; };
+template <class X, class Y> struct gr_is_same { static constexpr bool value = false; };
+template <class X> struct gr_is_same<X, X> { static constexpr bool value = true; };
 
 // Swap bits 2 and 3 of a row index inside a 32-row MFMA block.
 __device__ __forceinline__ int gr_perm32(int r) {
@@ -326,6 +330,25 @@ __device__ __forceinline__ void gr_flash_qk(gr_f32x16 (&s)[BN / 32][QB], const c
     }
 }
 
+// gr_flash_qk with the accumulators starting from ci[qb] instead of zero: each
+// score comes out as q.k - base in one MFMA chain.
+template <class T, int D, int BN, int QB, bool KTR = false>
+__device__ __forceinline__ void gr_flash_qk_from(gr_f32x16 (&s)[BN / 32][QB], const char* ks,
+                                                 const typename gr_mfma<T>::vec8 (&qf)[QB][D / 16],
+                                                 const gr_f32x16 (&ci)[QB], int l32, int g) {
+  typedef typename gr_mfma<T>::vec8 vec8;
+#pragma unroll
+  for (int ds = 0; ds < D / 16; ++ds)
+#pragma unroll
+    for (int kb = 0; kb < BN / 32; ++kb) {
+      const int row = kb * 32 + l32;
+      const vec8 af = KTR ? gr_tr_frag<T, BN, true>(ks, ds * 16, kb * 32, l32 + 32 * g)
+                          : gr_as<vec8>(gr_ld16(ks + row * (D * 2) + gr_swz<D / 8>(row, 2 * ds + g) * 16));
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) s[kb][qb] = gr_mfma<T>::mma32(af, qf[qb][ds], ds == 0 ? ci[qb] : s[kb][qb]);
+    }
+}
+
 template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT, bool PIPE, bool TR = false,
           bool DIRECT = false, bool SPLIT = false>
 __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* lds) {
@@ -369,6 +392,24 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds)
       qf[qb][ds] = gr_as<vec8>(gr_ld16(Qp + (long long)gr_imin(qw + qb * 32 + l32, Nq - 1) * a.q_sn + ds * 16 + 8 * g));
+  // CI (the straight schedule with transposing reads, GR_FLASH_OPT): Q is
+  // pre-scaled by c = scale log2(e) (rounded to T once: relative 2^-11 in fp16,
+  // 2^-8 in bf16) and the score MFMAs start from -base, so the scores come out
+  // as exponents of 2 relative to the base and p = 2^s needs no VALU multiply-
+  // add per score. m then holds the base in those units (scale log2(e) q.k).
+  // fp16 only: bf16 keeps Q as given.
+  constexpr bool CI = GR_FLASH_OPT && !PIPE && TR && gr_is_same<T, _Float16>::value;
+  gr_f32x16 cinit[QB];
+  if constexpr (CI) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      cinit[qb] = (gr_f32x16)(0.f);
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[qb][ds][e] = (T)((float)qf[qb][ds][e] * a.scale_log2);
+    }
+  }
 
   gr_f32x16 o[DB][QB];
   float m[QB], l[QB];
@@ -461,8 +502,7 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
     if (wave_active(t)) {
       // this tile's scores (with PIPE they were computed in the previous
       // iteration) and, on the diagonal of a causal block, the mask
-      auto scores = [&]() {
-        if constexpr (!PIPE) gr_flash_qk<T, D, BN, QB, KTR>(s, ks0 + ODD * L::KS, qf, l32, g);
+      auto mask = [&]() {
         if (CAUSAL && k0 + BN - 1 > qw) {
 #pragma unroll
           for (int kb = 0; kb < KB; ++kb)
@@ -477,8 +517,95 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
             }
         }
       };
+      auto scores = [&]() {
+        if constexpr (!PIPE) gr_flash_qk<T, D, BN, QB, KTR>(s, ks0 + ODD * L::KS, qf, l32, g);
+        mask();
+      };
 #if GR_FLASH_OPT
+      if constexpr (CI) {
+        // P of the whole tile with the current base and no max pass; the max
+        // pass runs only on the first tile and when some p overflowed (then
+        // the base moves to the true max and P is recomputed, shifted).
+        vec8 pt[KB][2][QB];
+        float lt[QB];
+        auto make_p = [&](auto shift_tag, const float (&sh)[QB]) {
+          constexpr bool SHIFT = decltype(shift_tag)::value;
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) lt[qb] = 0.f;
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+              for (int qb = 0; qb < QB; ++qb) {
+                gr_u32x4 pw;
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                  const float x0 = SHIFT ? s[kb][qb][8 * hf + e] + sh[qb] : s[kb][qb][8 * hf + e];
+                  const float x1 = SHIFT ? s[kb][qb][8 * hf + e + 1] + sh[qb] : s[kb][qb][8 * hf + e + 1];
+                  const vec2 pp = __builtin_convertvector((gr_f32x2){gr_exp2(x0), gr_exp2(x1)}, vec2);
+                  lt[qb] = MF::sum2(pp, lt[qb]);
+                  pw[e >> 1] = __builtin_bit_cast(unsigned int, pp);
+                }
+                pt[kb][hf][qb] = gr_as<vec8>(pw);
+              }
+        };
+        gr_flash_qk_from<T, D, BN, QB, KTR>(s, ks0 + ODD * L::KS, qf, cinit, l32, g);
+        mask();
+        bool fresh = false;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) fresh |= m[qb] == -GR_INF;
+        bool ok = false;
+        if (!gr_any(fresh)) {
+          const float z[QB] = {};
+          make_p(gr_ic<0>{}, z);
+          bool bad = false;
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) bad |= !(lt[qb] <= 3.0e38f);   // an inf (or NaN) p
+          ok = !gr_any(bad);
+        }
+        if (!ok) {
+          float sh[QB];
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) {
+            const float bt = (m[qb] == -GR_INF) ? 0.f : m[qb];   // the base these scores are relative to
+            float mt = -GR_INF;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][qb][r]);
+            mt = fmaxf(mt, gr_xor32(mt));
+            const float mn = fmaxf(m[qb], mt + bt);
+            if (gr_any(mn > m[qb])) {
+              const float alpha = gr_exp2(m[qb] - mn);   // m = -inf -> 0
+              l[qb] *= alpha;
+#pragma unroll
+              for (int db = 0; db < DB; ++db) o[db][qb] *= alpha;
+              m[qb] = mn;
+            }
+            const float nb = (m[qb] == -GR_INF) ? 0.f : m[qb];
+            sh[qb] = bt - nb;
+            cinit[qb] = (gr_f32x16)(-nb);
+          }
+          make_p(gr_ic<1>{}, sh);
+        }
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) l[qb] += lt[qb];
+        const char* vt = vt0 + ODD * L::VT;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+              const vec8 vf = gr_tr_frag<T, D, false>(vt, kb * 32 + 16 * hf, db * 32, l32 + 32 * g);
+#pragma unroll
+              for (int qb = 0; qb < QB; ++qb) o[db][qb] = MF::mma32(vf, pt[kb][hf][qb], o[db][qb]);
+            }
+      } else
       if constexpr (!PIPE && TR) {
+        // bf16: Q is not pre-scaled (its rounding would cost 2^-8), one
+        // multiply-add per score instead
         // P of the whole tile with the current base; the max pass runs only on
         // the first tile and when some p overflowed (then the base moves to
         // the true max and P is recomputed).
@@ -673,7 +800,8 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
             const gr_f32x4 w = {o[db][qb][4 * rr], o[db][qb][4 * rr + 1], o[db][qb][4 * rr + 2], o[db][qb][4 * rr + 3]};
             *reinterpret_cast<gr_f32x4*>(po + db * 32 + 8 * rr + 4 * g) = w;
           }
-        if (g == 0) *reinterpret_cast<gr_f32x2*>(a.part_ml + (part * Nq + q) * 2) = (gr_f32x2){m[qb], lt};
+        // m in units of q.k (the merge kernel scales by c)
+        if (g == 0) *reinterpret_cast<gr_f32x2*>(a.part_ml + (part * Nq + q) * 2) = (gr_f32x2){CI ? m[qb] / c : m[qb], lt};
       }
     }
     return;
@@ -684,7 +812,8 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
     const float inv = 1.0f / lt;
     if (qw + qb * 32 + l32 >= Nq) continue;
     // log-sum-exp of scale * s: p = 2^((s - m) c) with c = scale log2(e)
-    if (a.lse && g == 0) a.lse[(long long)bh * Nq + qw + qb * 32 + l32] = (m[qb] * c + __builtin_amdgcn_logf(lt)) * 0.6931471805599453f;
+    if (a.lse && g == 0)
+      a.lse[(long long)bh * Nq + qw + qb * 32 + l32] = ((CI ? m[qb] : m[qb] * c) + __builtin_amdgcn_logf(lt)) * 0.6931471805599453f;
     T* orow = Op + (long long)(qw + qb * 32 + l32) * a.o_sn;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
