@@ -329,8 +329,21 @@ def run_descent(cfg, seconds: float, seed: int):
             "compiled_variants": st["compiled_variants"], "cache_hits": st["cache_hits"],
             "evals_per_min": round(60.0 * st["timed_variants"] / max(wall, 1e-9), 1),
             "best_loss_ms": round(ev(best), 6), "start": "naive 8-stage program, full-extent tiles",
-            "stages": [[l.out, list(l.tile_shape)] for l in best.body]}
+            "stages": [[l.out, list(l.tile_shape)] for l in best.body],
+            "best_so_far": best_so_far(ev.timeline, cfg.flops)}
     return best, info
+
+
+def best_so_far(timeline, flops: float) -> list:
+    """[seconds, timed variants, best ms, best TFLOP/s] at every improvement of
+    the best timed variant of a descent (from the Evaluator's timeline)."""
+    out, best = [], math.inf
+    for n, e in enumerate(timeline, 1):
+        ms = e["loss"]
+        if 0 < ms < best:
+            best = ms
+            out.append([round(e["t"], 2), n, round(ms, 6), round(flops / (ms * 1e-3) / 1e12, 1)])
+    return out
 
 
 def main() -> int:

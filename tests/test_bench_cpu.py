@@ -59,3 +59,14 @@ def test_save_best_round_trip(tmp_path):
     assert again["key"] == saved["key"] and again["stages"] == saved["stages"]
     assert [lw[:2] for lw in again["lowering"]] == [lw[:2] for lw in saved["lowering"]]
     assert (again["best_loss_ms"], again["iterations"], again["timed_variants"]) == (1.0, 7, 3)
+
+
+def test_best_so_far_curve_keeps_improvements_only():
+    sys.path.insert(0, REPO)
+    import bench
+    timeline = [{"t": 0.5, "loss": 0.3}, {"t": 1.0, "loss": 0.5}, {"t": 1.2, "loss": float("inf")},
+                {"t": 1.5, "loss": 0.1}, {"t": 2.0, "loss": 0.1}]
+    curve = bench.best_so_far(timeline, 1e12)
+    assert [p[1] for p in curve] == [1, 4]          # variant index of each improvement
+    assert [p[2] for p in curve] == [0.3, 0.1]      # best ms, strictly decreasing
+    assert curve[-1][3] == round(1e12 / 0.1e-3 / 1e12, 1)
