@@ -806,14 +806,23 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
     }
     return;
   }
+  // O = O^T^T / l. A lane holds 4 x 8 bytes of its query's row per 32 head
+  // dims; written as they are, every store instruction touches 32 rows. When
+  // the LDS ring can hold the workgroup's O tile (it is free after the last
+  // tile's barrier), each wave stages its 32 x D block there and stores whole
+  // 16-byte chunks of consecutive rows instead (8 rows of 128 bytes per
+  // instruction at d = 64).
+  constexpr int CPR = D / 8;
+  constexpr bool STAGE_O = L::BYTES >= NW * QB * 32 * D * 2;
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const float lt = l[qb] + gr_xor32(l[qb]);
     const float inv = 1.0f / lt;
-    if (qw + qb * 32 + l32 >= Nq) continue;
+    const bool live = qw + qb * 32 + l32 < Nq;
     // log-sum-exp of scale * s: p = 2^((s - m) c) with c = scale log2(e)
-    if (a.lse && g == 0)
+    if (live && a.lse && g == 0)
       a.lse[(long long)bh * Nq + qw + qb * 32 + l32] = ((CI ? m[qb] : m[qb] * c) + __builtin_amdgcn_logf(lt)) * 0.6931471805599453f;
+    char* const stage = lds + (wave * QB + qb) * (32 * D * 2);
     T* orow = Op + (long long)(qw + qb * 32 + l32) * a.o_sn;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
@@ -822,8 +831,21 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
         const unsigned int w0 = gr_pack2<T>((T)(o[db][qb][4 * rr + 0] * inv), (T)(o[db][qb][4 * rr + 1] * inv));
         const unsigned int w1 = gr_pack2<T>((T)(o[db][qb][4 * rr + 2] * inv), (T)(o[db][qb][4 * rr + 3] * inv));
         gr_u32x2 w = {w0, w1};
-        *reinterpret_cast<gr_u32x2*>(orow + db * 32 + 8 * rr + 4 * g) = w;
+        if constexpr (STAGE_O)
+          *reinterpret_cast<gr_u32x2*>(stage + l32 * (D * 2) + gr_swz<CPR>(l32, db * 4 + rr) * 16 + g * 8) = w;
+        else if (live)
+          *reinterpret_cast<gr_u32x2*>(orow + db * 32 + 8 * rr + 4 * g) = w;
       }
+    if constexpr (STAGE_O) {
+      __builtin_amdgcn_wave_barrier();   // this wave's LDS writes precede its reads (in order per wave)
+#pragma unroll
+      for (int it = 0; it < 32 * CPR / 64; ++it) {
+        const int j = it * 64 + lane, row = j / CPR, ch = j % CPR;
+        const gr_u32x4 v = gr_ld16(stage + row * (D * 2) + gr_swz<CPR>(row, ch) * 16);
+        if (qw + qb * 32 + row < Nq)
+          *reinterpret_cast<gr_u32x4*>(Op + (long long)(qw + qb * 32 + row) * a.o_sn + ch * 8) = v;
+      }
+    }
   }
 }
 
