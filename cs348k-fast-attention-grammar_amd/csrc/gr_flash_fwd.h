@@ -386,12 +386,36 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
   const int qw = q0 + wave * (QB * 32);
   const float c = a.scale_log2;
 
+  // Q fragments (8 consecutive d of one query per lane). STAGE_Q: each wave
+  // loads its 32-query blocks straight into the LDS slots the second key tile
+  // will use (whole rows, 16 bytes per lane) and reads its fragments from
+  // there before the prologue barrier; else a lane loads its fragments from
+  // global memory directly (every load then touches 32 rows).
+  constexpr int QBLK = 32 * D * 2;
+  constexpr bool STAGE_Q = DIRECT && !PIPE && NW * QB <= 2 * KB;
   vec8 qf[QB][DS];
+  if constexpr (!STAGE_Q) {
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb)
+    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds)
-      qf[qb][ds] = gr_as<vec8>(gr_ld16(Qp + (long long)gr_imin(qw + qb * 32 + l32, Nq - 1) * a.q_sn + ds * 16 + 8 * g));
+      for (int ds = 0; ds < DS; ++ds)
+        qf[qb][ds] = gr_as<vec8>(gr_ld16(Qp + (long long)gr_imin(qw + qb * 32 + l32, Nq - 1) * a.q_sn + ds * 16 + 8 * g));
+  }
+  auto q_stage = [&](int qb) -> char* {
+    // K slot 1, then V slot 1, KB blocks each; wave-uniform (an SGPR for the
+    // direct loads' LDS base)
+    const int idx = __builtin_amdgcn_readfirstlane(wave) * QB + qb;
+    return (idx < KB ? lds + L::KS : lds + 2 * L::KS + L::VT) + (idx % KB) * QBLK;
+  };
+  if constexpr (STAGE_Q) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      gr_lds_loader<T, 32, D, 64> ql;
+      const int rows = Nq - (qw + qb * 32);
+      ql.init(lane, a.q_sn, rows < 1 ? 1 : (rows > 32 ? 32 : rows));
+      ql.load(Qp + (long long)(qw + qb * 32 < Nq ? qw + qb * 32 : Nq - 1) * a.q_sn, q_stage(qb));
+    }
+  }
   // CI (the straight schedule with transposing reads, GR_FLASH_OPT): Q is
   // pre-scaled by c = scale log2(e) (rounded to T once: relative 2^-11 in fp16,
   // 2^-8 in bf16) and the score MFMAs start from -base, so the scores come out
@@ -400,16 +424,18 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
   // fp16 only: bf16 keeps Q as given.
   constexpr bool CI = GR_FLASH_OPT && !PIPE && TR && gr_is_same<T, _Float16>::value;
   gr_f32x16 cinit[QB];
-  if constexpr (CI) {
+  auto prescale_q = [&]() {
+    if constexpr (CI) {
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      cinit[qb] = (gr_f32x16)(0.f);
+      for (int qb = 0; qb < QB; ++qb) {
+        cinit[qb] = (gr_f32x16)(0.f);
 #pragma unroll
-      for (int ds = 0; ds < DS; ++ds)
+        for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qf[qb][ds][e] = (T)((float)qf[qb][ds][e] * a.scale_log2);
+          for (int e = 0; e < 8; ++e) qf[qb][ds][e] = (T)((float)qf[qb][ds][e] * a.scale_log2);
+      }
     }
-  }
+  };
 
   gr_f32x16 o[DB][QB];
   float m[QB], l[QB];
@@ -473,7 +499,17 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
   // back edge that they completed, and would otherwise wait on the vmcnt of
   // the in-flight next-tile prefetch at the first score MFMA of every tile.
   __builtin_amdgcn_s_waitcnt(0);
+  if constexpr (STAGE_Q) {
+    // this wave's own Q blocks (its loads have landed: vmcnt is 0); the
+    // barrier below orders these reads before the next tile's prefetch
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds)
+        qf[qb][ds] = gr_as<vec8>(gr_ld16(q_stage(qb) + l32 * (D * 2) + gr_swz<D / 8>(l32, 2 * ds + g) * 16));
+  }
   __syncthreads();
+  prescale_q();
   // Two score buffers used in turn (the loop is unrolled by two), so handing
   // the next tile's scores over costs no register moves.
   gr_f32x16 sA[KB][QB], sB[PIPE ? KB : 1][QB];
