@@ -44,6 +44,34 @@ struct gr_attn_bwd_args {
   float scale;
 };
 
+// Store a wave's 32 x D block whose transpose sits in MFMA accumulators
+// (acc[db] register r: row l32, column db*32 + 8(r/4) + 4g + r%4), times mul,
+// as rows of T: staged through this wave's 32*D*2 bytes of free LDS, so the
+// global stores are whole 16-byte chunks of consecutive rows (row r at
+// dst + r*ld).
+template <class T, int D>
+__device__ __forceinline__ void gr_store_block_t(const gr_f32x16 (&acc)[D / 32], float mul, char* stage, T* dst,
+                                                 long long ld, int lane) {
+  constexpr int CPR = D / 8;
+  const int g = lane >> 5, l32 = lane & 31;
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      gr_u32x2 w;
+      w[0] = gr_pack2<T>((T)(acc[db][4 * rr] * mul), (T)(acc[db][4 * rr + 1] * mul));
+      w[1] = gr_pack2<T>((T)(acc[db][4 * rr + 2] * mul), (T)(acc[db][4 * rr + 3] * mul));
+      *reinterpret_cast<gr_u32x2*>(stage + l32 * (D * 2) + gr_swz<CPR>(l32, db * 4 + rr) * 16 + g * 8) = w;
+    }
+  __builtin_amdgcn_wave_barrier();   // LDS writes and reads of one wave stay in order
+#pragma unroll
+  for (int it = 0; it < 32 * CPR / 64; ++it) {
+    const int j = it * 64 + lane, row = j / CPR, ch = j % CPR;
+    *reinterpret_cast<gr_u32x4*>(dst + (long long)row * ld + ch * 8) =
+        gr_ld16(stage + row * (D * 2) + gr_swz<CPR>(row, ch) * 16);
+  }
+}
+
 template <int D, int BM>
 struct gr_attn_bwd_lds {
   static constexpr int QT = BM * D * 2;          // one Q or dO tile
@@ -169,22 +197,13 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
     __syncthreads();
   }
 
-  // dK = scale dK^T^T, dV = dV^T^T: lane holds key kw0 + l32, d rows 8(r/4) + 4g + r%4 of block db
-  T* dk = static_cast<T*>(a.dk) + base + (long long)(kw0 + l32) * a.sn;
-  T* dv = static_cast<T*>(a.dv) + base + (long long)(kw0 + l32) * a.sn;
-#pragma unroll
-  for (int db = 0; db < DB; ++db)
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int d = db * 32 + 8 * rr + 4 * g;
-      gr_u32x2 wk, wv;
-      wk[0] = gr_pack2<T>((T)(dkt[db][4 * rr] * a.scale), (T)(dkt[db][4 * rr + 1] * a.scale));
-      wk[1] = gr_pack2<T>((T)(dkt[db][4 * rr + 2] * a.scale), (T)(dkt[db][4 * rr + 3] * a.scale));
-      wv[0] = gr_pack2<T>((T)dvt[db][4 * rr], (T)dvt[db][4 * rr + 1]);
-      wv[1] = gr_pack2<T>((T)dvt[db][4 * rr + 2], (T)dvt[db][4 * rr + 3]);
-      *reinterpret_cast<gr_u32x2*>(dk + d) = wk;
-      *reinterpret_cast<gr_u32x2*>(dv + d) = wv;
-    }
+  // dK = scale dK^T^T, dV = dV^T^T for keys kw0.. (the LDS stages are free
+  // after the last tile's barrier: 2 * 32 * D * 2 bytes per wave)
+  static_assert(NW * 2 * 32 * D * 2 <= L::BYTES, "dK/dV staging fits the LDS stages");
+  char* const stage = lds + wave * (2 * 32 * D * 2);
+  gr_store_block_t<T, D>(dkt, a.scale, stage, static_cast<T*>(a.dk) + base + (long long)kw0 * a.sn, a.sn, lane);
+  gr_store_block_t<T, D>(dvt, 1.0f, stage + 32 * D * 2, static_cast<T*>(a.dv) + base + (long long)kw0 * a.sn, a.sn,
+                         lane);
 }
 
 template <int D, int BN>
@@ -308,15 +327,8 @@ void gr_attn_bwd_dq_kernel(gr_attn_bwd_args a) {
     __syncthreads();
   }
 
-  // dQ = scale dQ^T^T: lane holds query myq, d rows 8(r/4) + 4g + r%4 of block db
-  T* dq = static_cast<T*>(a.dq) + base + (long long)myq * a.sn;
-#pragma unroll
-  for (int db = 0; db < DB; ++db)
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      gr_u32x2 w;
-      w[0] = gr_pack2<T>((T)(dqt[db][4 * rr] * a.scale), (T)(dqt[db][4 * rr + 1] * a.scale));
-      w[1] = gr_pack2<T>((T)(dqt[db][4 * rr + 2] * a.scale), (T)(dqt[db][4 * rr + 3] * a.scale));
-      *reinterpret_cast<gr_u32x2*>(dq + db * 32 + 8 * rr + 4 * g) = w;
-    }
+  // dQ = scale dQ^T^T for queries qw.. (staged in the free LDS stages)
+  static_assert(NW * 32 * D * 2 <= L::BYTES, "dQ staging fits the LDS stages");
+  gr_store_block_t<T, D>(dqt, a.scale, lds + wave * (32 * D * 2), static_cast<T*>(a.dq) + base + (long long)qw * a.sn,
+                         a.sn, lane);
 }
