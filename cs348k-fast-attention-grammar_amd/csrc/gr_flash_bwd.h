@@ -48,7 +48,7 @@ struct gr_attn_bwd_args {
 // (acc[db] register r: row l32, column db*32 + 8(r/4) + 4g + r%4), times mul,
 // as rows of T: staged through this wave's 32*D*2 bytes of free LDS, so the
 // global stores are whole 16-byte chunks of consecutive rows (row r at
-// dst + r*ld).
+// dst + r*ld), streamed past the caches (nontemporal).
 template <class T, int D>
 __device__ __forceinline__ void gr_store_block_t(const gr_f32x16 (&acc)[D / 32], float mul, char* stage, T* dst,
                                                  long long ld, int lane) {
@@ -67,8 +67,8 @@ __device__ __forceinline__ void gr_store_block_t(const gr_f32x16 (&acc)[D / 32],
 #pragma unroll
   for (int it = 0; it < 32 * CPR / 64; ++it) {
     const int j = it * 64 + lane, row = j / CPR, ch = j % CPR;
-    *reinterpret_cast<gr_u32x4*>(dst + (long long)row * ld + ch * 8) =
-        gr_ld16(stage + row * (D * 2) + gr_swz<CPR>(row, ch) * 16);
+    __builtin_nontemporal_store(gr_ld16(stage + row * (D * 2) + gr_swz<CPR>(row, ch) * 16),
+                                reinterpret_cast<gr_u32x4*>(dst + (long long)row * ld + ch * 8));
   }
 }
 

@@ -878,8 +878,8 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
       for (int it = 0; it < 32 * CPR / 64; ++it) {
         const int j = it * 64 + lane, row = j / CPR, ch = j % CPR;
         const gr_u32x4 v = gr_ld16(stage + row * (D * 2) + gr_swz<CPR>(row, ch) * 16);
-        if (qw + qb * 32 + row < Nq)
-          *reinterpret_cast<gr_u32x4*>(Op + (long long)(qw + qb * 32 + row) * a.o_sn + ch * 8) = v;
+        if (qw + qb * 32 + row < Nq)   // streamed past the caches: nothing here reads O back
+          __builtin_nontemporal_store(v, reinterpret_cast<gr_u32x4*>(Op + (long long)(qw + qb * 32 + row) * a.o_sn + ch * 8));
       }
     }
   }
