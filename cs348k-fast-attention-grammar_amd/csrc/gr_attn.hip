@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) void gr_attn_combine_kernel(const float* __res
   const float inv = 1.0f / L;
   gr_u32x4 out;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) out[e] = gr_pack2<T>((T)(acc[2 * e] * inv), (T)(acc[2 * e + 1] * inv));
+  for (int e = 0; e < 4; ++e) out[e] = gr_pack2f<T>(acc[2 * e] * inv, acc[2 * e + 1] * inv);
   const int b = bh / H, h = bh % H;
   gr_st16(o + b * o_sb + h * o_sh + (long long)q * o_sn + ch * 8, out);
 }

@@ -125,6 +125,14 @@ __device__ __forceinline__ float gr_xor32(float v) {
 // 2^x on the transcendental unit (v_exp_f32); overflows to +inf, -inf gives 0.
 __device__ __forceinline__ float gr_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Round two floats to the storage type and pack them into one dword (low = a,
+// high = b): one v_cvt_pk_{f16,bf16}_f32 on gfx950.
+template <class T>
+__device__ __forceinline__ unsigned int gr_pack2f(float a, float b) {
+  typedef T t2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(unsigned int, __builtin_convertvector((gr_f32x2){a, b}, t2));
+}
+
 // Pack two storage-type values into one dword (low = a, high = b).
 template <class T>
 __device__ __forceinline__ unsigned int gr_pack2(T a, T b) {

@@ -59,8 +59,8 @@ __device__ __forceinline__ void gr_store_block_t(const gr_f32x16 (&acc)[D / 32],
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       gr_u32x2 w;
-      w[0] = gr_pack2<T>((T)(acc[db][4 * rr] * mul), (T)(acc[db][4 * rr + 1] * mul));
-      w[1] = gr_pack2<T>((T)(acc[db][4 * rr + 2] * mul), (T)(acc[db][4 * rr + 3] * mul));
+      w[0] = gr_pack2f<T>(acc[db][4 * rr] * mul, acc[db][4 * rr + 1] * mul);
+      w[1] = gr_pack2f<T>(acc[db][4 * rr + 2] * mul, acc[db][4 * rr + 3] * mul);
       *reinterpret_cast<gr_u32x2*>(stage + l32 * (D * 2) + gr_swz<CPR>(l32, db * 4 + rr) * 16 + g * 8) = w;
     }
   __builtin_amdgcn_wave_barrier();   // LDS writes and reads of one wave stay in order
@@ -160,7 +160,14 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
         sa = MF::mma32(qa, kf[ds], sa);
         dpa = MF::mma32(da, vf[ds], dpa);
       }
-      // register r holds query j*32 + 8g + r (r < 8) or j*32 + 16 + 8g + r - 8
+      // register r holds query j*32 + 8g + r (r < 8) or j*32 + 16 + 8g + r - 8.
+      // Causal: only a block whose queries start below the wave's last key
+      // is masked (a wave-uniform branch; p = 2^-inf = 0 where key > query).
+      if (CAUSAL && kw0 + 31 > q0 + j * 32) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (kw0 + l32 > q0 + j * 32 + 16 * (r >> 3) + 8 * g + (r & 7)) sa[r] = -GR_INF;
+      }
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf) {
         gr_u32x4 pw, dw;
@@ -171,13 +178,12 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
           for (int u = 0; u < 2; ++u) {
             const int r = 8 * hf + e + u;
             const int ql_ = j * 32 + 16 * hf + 8 * g + e + u;
-            float p = gr_exp2(sa[r] * c - lse2[ql_]);
-            if (CAUSAL && kw0 + l32 > q0 + ql_) p = 0.f;
+            const float p = gr_exp2(sa[r] * c - lse2[ql_]);
             p2[u] = p;
             d2[u] = p * (dpa[r] - dlt[ql_]);
           }
-          pw[e >> 1] = gr_pack2<T>((T)p2[0], (T)p2[1]);
-          dw[e >> 1] = gr_pack2<T>((T)d2[0], (T)d2[1]);
+          pw[e >> 1] = gr_pack2f<T>(p2[0], p2[1]);
+          dw[e >> 1] = gr_pack2f<T>(d2[0], d2[1]);
         }
         pb[j][hf] = gr_as<vec8>(pw);
         dsb[j][hf] = gr_as<vec8>(dw);
@@ -298,7 +304,14 @@ void gr_attn_bwd_dq_kernel(gr_attn_bwd_args a) {
           sa = MF::mma32(gr_as<vec8>(gr_ld16(ks + row * (D * 2) + ch * 16)), qf[ds], sa);
           dpa = MF::mma32(gr_as<vec8>(gr_ld16(vs + row * (D * 2) + ch * 16)), df[ds], dpa);
         }
-        // register r: key k0 + kb*32 + 8g + r (r < 8) or + 16 + 8g + r - 8
+        // register r: key k0 + kb*32 + 8g + r (r < 8) or + 16 + 8g + r - 8;
+        // causal: only a key block that reaches past the wave's first query
+        // is masked (wave-uniform branch)
+        if (CAUSAL && k0 + kb * 32 + 31 > qw) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (k0 + kb * 32 + 16 * (r >> 3) + 8 * g + (r & 7) > myq) sa[r] = -GR_INF;
+        }
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
           gr_u32x4 dw;
@@ -308,11 +321,10 @@ void gr_attn_bwd_dq_kernel(gr_attn_bwd_args a) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
               const int r = 8 * hf + e + u;
-              float p = gr_exp2(sa[r] * c - lse2);
-              if (CAUSAL && k0 + kb * 32 + 16 * hf + 8 * g + e + u > myq) p = 0.f;
+              const float p = gr_exp2(sa[r] * c - lse2);
               d2[u] = p * (dpa[r] - dlt);
             }
-            dw[e >> 1] = gr_pack2<T>((T)d2[0], (T)d2[1]);
+            dw[e >> 1] = gr_pack2f<T>(d2[0], d2[1]);
           }
           const vec8 dsb = gr_as<vec8>(dw);
 #pragma unroll

@@ -864,8 +864,8 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const unsigned int w0 = gr_pack2<T>((T)(o[db][qb][4 * rr + 0] * inv), (T)(o[db][qb][4 * rr + 1] * inv));
-        const unsigned int w1 = gr_pack2<T>((T)(o[db][qb][4 * rr + 2] * inv), (T)(o[db][qb][4 * rr + 3] * inv));
+        const unsigned int w0 = gr_pack2f<T>(o[db][qb][4 * rr + 0] * inv, o[db][qb][4 * rr + 1] * inv);
+        const unsigned int w1 = gr_pack2f<T>(o[db][qb][4 * rr + 2] * inv, o[db][qb][4 * rr + 3] * inv);
         gr_u32x2 w = {w0, w1};
         if constexpr (STAGE_O)
           *reinterpret_cast<gr_u32x2*>(stage + l32 * (D * 2) + gr_swz<CPR>(l32, db * 4 + rr) * 16 + g * 8) = w;

@@ -186,10 +186,10 @@ __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
       for (int q = 0; q < 4; ++q) {
         const int chunk = (wn * G::WN + i * 32 + 8 * q) >> 3;
         gr_u32x2 w;
-        w[0] = gr_pack2<T>((T)gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + 0]),
-                           (T)gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + 1]));
-        w[1] = gr_pack2<T>((T)gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + 2]),
-                           (T)gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + 3]));
+        w[0] = gr_pack2f<T>(gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + 0]),
+                            gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + 1]));
+        w[1] = gr_pack2f<T>(gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + 2]),
+                            gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + 3]));
         *reinterpret_cast<gr_u32x2*>(lds + row * (BN * 2) + gr_swz<OCPR>(row, chunk) * 16 + g * 8) = w;
       }
   }
