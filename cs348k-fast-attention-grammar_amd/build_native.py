@@ -30,6 +30,14 @@ COMMON = [
 ]
 
 
+# Per-source extra flags. The backward's d = 128 dK/dV kernel runs one wave
+# per SIMD; left to its heuristics the backend then puts every MFMA
+# accumulator in AGPRs and copies the score accumulators to VGPRs (and back)
+# for the softmax arithmetic on every tile. VGPR-form MFMAs need no copies and
+# fit in 245 VGPRs (the d = 64 kernels are faster with the heuristics).
+EXTRA = {"gr_attn_bwd128.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _sources() -> list[str]:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC)
                   if f.endswith((".hip", ".cpp")))
@@ -37,7 +45,7 @@ def _sources() -> list[str]:
 
 def _compile(src: str) -> str:
     obj = os.path.join(OBJDIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *COMMON, "-c", src, "-o", obj]
+    cmd = [HIPCC, *COMMON, *EXTRA.get(os.path.basename(src), []), "-c", src, "-o", obj]
     if src.endswith(".cpp"):
         cmd[1:1] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -4,7 +4,7 @@
 
 #include <cstdint>
 
-#include "gr_flash_bwd.h"
+#include "gr_flash_fwd.h"
 #include "gr_host.h"
 #include "grammar_rt.h"
 
@@ -222,34 +222,6 @@ int attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, i
   return gr::fail(GR_E_ARG, "gr_attn_fwd: dtype %d unsupported (GR_F16 or GR_BF16)", dtype);
 }
 
-// Backward tiles. dK/dV: (queries per tile, keys per workgroup) = (64, 128),
-// one wave per 32 keys. dQ: key tiles of 64, 8 waves (256 queries) per
-// workgroup when N allows it, else 4.
-template <class T, int D, int NW>
-void launch_bwd_dq(const gr_attn_bwd_args& a, bool causal, hipStream_t st) {
-  constexpr int DQ_BN = 64;
-  const dim3 grid((unsigned)((long long)a.B * a.H * (a.N / (NW * 32))));
-  constexpr int LDS = gr_attn_bwd_dq_lds<D, DQ_BN>::BYTES;
-  if (causal) hipLaunchKernelGGL((gr_attn_bwd_dq_kernel<T, D, NW, DQ_BN, true>), grid, dim3(NW * 64), LDS, st, a);
-  else hipLaunchKernelGGL((gr_attn_bwd_dq_kernel<T, D, NW, DQ_BN, false>), grid, dim3(NW * 64), LDS, st, a);
-}
-
-template <class T, int D, int BM, int BN>
-int launch_bwd(const gr_attn_bwd_args& a, bool causal, hipStream_t st) {
-  if (a.N % BN != 0 || a.N % BM != 0 || a.N % 128 != 0)
-    return gr::fail(GR_E_ARG, "gr_attn_bwd: N=%d must be a multiple of %d at D=%d", a.N, BN > 128 ? BN : 128, D);
-  // dQ first: it also writes delta, which the dK/dV kernel reads
-  if (a.N % 256 == 0) launch_bwd_dq<T, D, 8>(a, causal, st);
-  else launch_bwd_dq<T, D, 4>(a, causal, st);
-  int rc = gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd dQ launch");
-  if (rc) return rc;
-  const dim3 grid((unsigned)((long long)a.B * a.H * (a.N / BN)));
-  constexpr int LDS = gr_attn_bwd_lds<D, BM>::BYTES;
-  if (causal) hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, true>), grid, dim3(BN / 32 * 64), LDS, st, a);
-  else hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, false>), grid, dim3(BN / 32 * 64), LDS, st, a);
-  return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd dK/dV launch");
-}
-
 }  // namespace
 
 extern "C" int gr_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H, int N,
@@ -266,59 +238,6 @@ extern "C" int gr_attn_fwd_train(const void* q, const void* k, const void* v, vo
   if (!lse || ((uintptr_t)lse & 3)) return gr::fail(GR_E_ARG, "gr_attn_fwd_train: lse must be a 4-byte aligned buffer");
   return attn_fwd(q, k, v, o, lse, dtype, B, H, N, D, qs, ks, vs, os, k_transposed, causal, scale, block_m, block_n,
                   stream);
-}
-
-extern "C" size_t gr_attn_bwd_workspace(int B, int H, int N, int D) {
-  if (B <= 0 || H <= 0 || N <= 0 || D <= 0) return 0;
-  return (size_t)B * H * N * sizeof(float);
-}
-
-extern "C" int gr_attn_bwd(const void* q, const void* k, const void* v, const void* o, const void* dout,
-                           const float* lse, void* dq, void* dk, void* dv, int dtype, int B, int H, int N, int D,
-                           const long long* strides, int causal, float scale, void* workspace, size_t workspace_bytes,
-                           void* stream) {
-  if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv || !strides)
-    return gr::fail(GR_E_ARG, "gr_attn_bwd: null argument");
-  if (B <= 0 || H <= 0 || N <= 0) return gr::fail(GR_E_ARG, "gr_attn_bwd: B, H, N must be positive");
-  const void* ptrs[10] = {q, k, v, o, dout, dq, dk, dv, workspace, lse};
-  for (int i = 0; i < 9; ++i)
-    if (!aligned16(ptrs[i])) return gr::fail(GR_E_ARG, "gr_attn_bwd: tensors and workspace must be 16-byte aligned");
-  if ((uintptr_t)lse & 3) return gr::fail(GR_E_ARG, "gr_attn_bwd: lse must be 4-byte aligned");
-  for (int i = 0; i < 3; ++i)
-    if (strides[i] < 0 || strides[i] % 8 != 0)
-      return gr::fail(GR_E_ARG, "gr_attn_bwd: strides must be non-negative multiples of 8 elements");
-  if (!(scale > 0.f)) return gr::fail(GR_E_ARG, "gr_attn_bwd: scale must be positive");
-  const size_t need = gr_attn_bwd_workspace(B, H, N, D);
-  if (!workspace || workspace_bytes < need)
-    return gr::fail(GR_E_ARG, "gr_attn_bwd: workspace of %zu bytes needed", need);
-  gr_attn_bwd_args a;
-  a.q = q;
-  a.k = k;
-  a.v = v;
-  a.o = o;
-  a.dout = dout;
-  a.lse = lse;
-  a.delta = static_cast<float*>(workspace);
-  a.dq = dq;
-  a.dk = dk;
-  a.dv = dv;
-  a.sb = strides[0];
-  a.sh = strides[1];
-  a.sn = strides[2];
-  a.B = B;
-  a.H = H;
-  a.N = N;
-  a.scale = scale;
-  hipStream_t st = (hipStream_t)stream;
-  const bool c = causal != 0;
-#define GR_BWD(TT)                                                               \
-  if (D == 64) return launch_bwd<TT, 64, 64, 128>(a, c, st);                     \
-  if (D == 128) return launch_bwd<TT, 128, 64, 128>(a, c, st);                   \
-  return gr::fail(GR_E_ARG, "gr_attn_bwd: head dim D=%d unsupported (64 or 128)", D);
-  if (dtype == GR_F16) { GR_BWD(_Float16) }
-  if (dtype == GR_BF16) { GR_BWD(__bf16) }
-#undef GR_BWD
-  return gr::fail(GR_E_ARG, "gr_attn_bwd: dtype %d unsupported (GR_F16 or GR_BF16)", dtype);
 }
 
 extern "C" int gr_selftest_mfma32(const void* a, const void* b, float* d, void* stream) {

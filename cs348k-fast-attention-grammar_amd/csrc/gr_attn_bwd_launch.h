@@ -1,0 +1,43 @@
+// gr_attn_bwd_launch.h -- launchers of the attention backward kernels
+// (host side, included by the translation units that instantiate them).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "gr_flash_bwd.h"
+#include "gr_host.h"
+#include "grammar_rt.h"
+
+namespace {
+
+// Backward tiles. dK/dV: (queries per tile, keys per workgroup) = (64, 128),
+// one wave per 32 keys. dQ: key tiles of 64, 8 waves (256 queries) per
+// workgroup when N allows it, else 4.
+template <class T, int D, int NW>
+void launch_bwd_dq(const gr_attn_bwd_args& a, bool causal, hipStream_t st) {
+  constexpr int DQ_BN = 64;
+  const dim3 grid((unsigned)((long long)a.B * a.H * (a.N / (NW * 32))));
+  constexpr int LDS = gr_attn_bwd_dq_lds<D, DQ_BN>::BYTES;
+  if (causal) hipLaunchKernelGGL((gr_attn_bwd_dq_kernel<T, D, NW, DQ_BN, true>), grid, dim3(NW * 64), LDS, st, a);
+  else hipLaunchKernelGGL((gr_attn_bwd_dq_kernel<T, D, NW, DQ_BN, false>), grid, dim3(NW * 64), LDS, st, a);
+}
+
+template <class T, int D, int BM, int BN>
+int launch_bwd(const gr_attn_bwd_args& a, bool causal, hipStream_t st) {
+  if (a.N % BN != 0 || a.N % BM != 0 || a.N % 128 != 0)
+    return gr::fail(GR_E_ARG, "gr_attn_bwd: N=%d must be a multiple of %d at D=%d", a.N, BN > 128 ? BN : 128, D);
+  // dQ first: it also writes delta, which the dK/dV kernel reads
+  if (a.N % 256 == 0) launch_bwd_dq<T, D, 8>(a, causal, st);
+  else launch_bwd_dq<T, D, 4>(a, causal, st);
+  int rc = gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd dQ launch");
+  if (rc) return rc;
+  const dim3 grid((unsigned)((long long)a.B * a.H * (a.N / BN)));
+  constexpr int LDS = gr_attn_bwd_lds<D, BM, BN>::BYTES;
+  if (causal) hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, true>), grid, dim3(BN / 32 * 64), LDS, st, a);
+  else hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, false>), grid, dim3(BN / 32 * 64), LDS, st, a);
+  return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd dK/dV launch");
+}
+
+}  // namespace
+
+// The d = 128 launches (gr_attn_bwd128.hip).
+int gr_attn_bwd_launch_d128(const gr_attn_bwd_args& a, bool bf16, bool causal, hipStream_t st);

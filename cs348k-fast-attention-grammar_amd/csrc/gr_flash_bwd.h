@@ -72,11 +72,21 @@ __device__ __forceinline__ void gr_store_block_t(const gr_f32x16 (&acc)[D / 32],
   }
 }
 
-template <int D, int BM>
+// LDS of the dK/dV kernel: two stages of (Q, dO, L, delta) tiles, then (KV_LDS,
+// d >= 128) each wave's 32 K and V rows: at d = 128 holding them in registers
+// as well as the dK/dV accumulators makes the allocator shuttle values
+// between VGPRs and AGPRs on every tile.
+template <int D, int BM, int BN>
 struct gr_attn_bwd_lds {
   static constexpr int QT = BM * D * 2;          // one Q or dO tile
   static constexpr int STAGE = 2 * QT + 2 * BM * 4;   // Q, dO, then log2-domain L and delta
-  static constexpr int BYTES = 2 * STAGE;
+  static constexpr int RING = 2 * STAGE;
+#ifndef GR_BWD_KV_LDS
+#define GR_BWD_KV_LDS 1
+#endif
+  static constexpr bool KV_LDS = GR_BWD_KV_LDS && D >= 128;
+  static constexpr int KVW = 2 * 32 * D * 2;     // one wave's K and V rows
+  static constexpr int BYTES = RING + (KV_LDS ? (BN / 32) * KVW : 0);
 };
 
 template <class T, int D, int BM, int BN, bool CAUSAL>
@@ -86,7 +96,7 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
   typedef typename MF::vec8 vec8;
   constexpr int NW = BN / 32, NT = NW * 64;
   constexpr int DS = D / 16, DB = D / 32, QJ = BM / 32;
-  typedef gr_attn_bwd_lds<D, BM> L;
+  typedef gr_attn_bwd_lds<D, BM, BN> L;
   static_assert(BM % 32 == 0 && BN % 32 == 0 && D % 32 == 0, "tile shape");
   static_assert(2 * BM <= NT, "one thread per statistic of a query tile");
   extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -105,13 +115,34 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
   const int kw0 = key0 + wave * 32;
   const float c = a.scale * 1.4426950408889634f;
 
-  // this wave's 32 keys as MFMA B operands (8 consecutive d per lane)
-  vec8 kf[DS], vf[DS];
+  // this wave's 32 keys as MFMA B operands (8 consecutive d per lane): in
+  // registers, or (KV_LDS) rows in LDS loaded straight from global memory and
+  // read per use
+  constexpr bool KVL = L::KV_LDS;
+  constexpr int CPR = D / 8;
+  vec8 kf[KVL ? 1 : DS], vf[KVL ? 1 : DS];
+  char* const kvs = lds + L::RING + __builtin_amdgcn_readfirstlane(wave) * L::KVW;
+  if constexpr (KVL) {
+    gr_lds_loader<T, 32, D, 64> kvl;
+    kvl.init(lane, a.sn);
+    kvl.load(K + (long long)kw0 * a.sn, kvs);
+    kvl.load(V + (long long)kw0 * a.sn, kvs + L::KVW / 2);
+  } else {
 #pragma unroll
-  for (int ds = 0; ds < DS; ++ds) {
-    kf[ds] = gr_as<vec8>(gr_ld16(K + (long long)(kw0 + l32) * a.sn + ds * 16 + 8 * g));
-    vf[ds] = gr_as<vec8>(gr_ld16(V + (long long)(kw0 + l32) * a.sn + ds * 16 + 8 * g));
+    for (int ds = 0; ds < DS; ++ds) {
+      kf[ds] = gr_as<vec8>(gr_ld16(K + (long long)(kw0 + l32) * a.sn + ds * 16 + 8 * g));
+      vf[ds] = gr_as<vec8>(gr_ld16(V + (long long)(kw0 + l32) * a.sn + ds * 16 + 8 * g));
+    }
   }
+  auto kfrag = [&](int ds) -> vec8 {
+    if constexpr (KVL) return gr_as<vec8>(gr_ld16(kvs + l32 * (D * 2) + gr_swz<CPR>(l32, 2 * ds + g) * 16));
+    else return kf[ds];
+  };
+  auto vfrag = [&](int ds) -> vec8 {
+    if constexpr (KVL)
+      return gr_as<vec8>(gr_ld16(kvs + L::KVW / 2 + l32 * (D * 2) + gr_swz<CPR>(l32, 2 * ds + g) * 16));
+    else return vf[ds];
+  };
   gr_f32x16 dkt[DB], dvt[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
@@ -157,8 +188,8 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
         const int ch = gr_swz_rt<D / 8>(row, 2 * ds + g);
         const vec8 qa = gr_as<vec8>(gr_ld16(qs + row * (D * 2) + ch * 16));
         const vec8 da = gr_as<vec8>(gr_ld16(dos + row * (D * 2) + ch * 16));
-        sa = MF::mma32(qa, kf[ds], sa);
-        dpa = MF::mma32(da, vf[ds], dpa);
+        sa = MF::mma32(qa, kfrag(ds), sa);
+        dpa = MF::mma32(da, vfrag(ds), dpa);
       }
       // register r holds query j*32 + 8g + r (r < 8) or j*32 + 16 + 8g + r - 8.
       // Causal: only a block whose queries start below the wave's last key
