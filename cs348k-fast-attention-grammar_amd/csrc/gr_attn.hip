@@ -4,7 +4,7 @@
 
 #include <cstdint>
 
-#include "gr_flash_fwd.h"
+#include "gr_flash_decode.h"
 #include "gr_host.h"
 #include "grammar_rt.h"
 
@@ -125,12 +125,45 @@ void decode_nw(const gr_attn_args& a, int nw, dim3 grid, hipStream_t st) {
   else decode_kernel<T, D, BN, 4, SPLIT>(a, grid, st);
 }
 
+template <class T, int D, int NQ>
+void decode_stream(const gr_attn_args& a, int S, hipStream_t st) {
+  constexpr int U = NQ == 1 ? 8 : 4;   // key-row loads of K and of V per lane and iteration
+  hipLaunchKernelGGL((gr_attn_decode_stream_kernel<T, D, NQ, U>), dim3((unsigned)(a.B * a.H), (unsigned)S),
+                     dim3(256), 0, st, a);
+}
+
 // Decode-shape launch: Nq queries (any count) against N keys, non-causal, K in
-// [B, H, N, D]; 32 queries per wave, up to 4 waves; 64-key tiles (32 when N
-// is not a multiple of 64); S > 1 splits the keys over S workgroups per query
-// tile and merges their partials through the workspace.
+// [B, H, N, D]. Up to 4 queries: the streaming kernel (gr_flash_decode.h),
+// one workgroup per head and key part. More: the flash body with 32 queries
+// per wave, up to 4 waves, 64-key tiles (32 when N is not a multiple of 64).
+// S > 1 splits the keys over S workgroups per head (or query tile) and merges
+// their partials through the workspace.
 template <class T, int D>
 int launch_decode(gr_attn_args a, int S, void* ws, size_t ws_bytes, hipStream_t st) {
+  if (a.Nq <= 4) {
+    if (S < 1) S = 1;
+    if (S > a.N / 32) S = a.N / 32;
+    a.kchunk = ((a.N / 32 + S - 1) / S) * 32;
+    S = (a.N + a.kchunk - 1) / a.kchunk;         // every part gets keys
+    if ((long long)a.B * a.H > 0x7fffffffLL || S > 65535) return gr::fail(GR_E_ARG, "gr_attn_decode: grid out of range");
+    if (S > 1) {
+      const size_t need = gr_attn_decode_workspace(a.B, a.H, a.Nq, D, S);
+      if (!ws || ws_bytes < need)
+        return gr::fail(GR_E_ARG, "gr_attn_decode: workspace of %zu bytes needed for %d key parts", need, S);
+      a.part_o = static_cast<float*>(ws);
+      a.part_ml = a.part_o + (size_t)S * a.B * a.H * a.Nq * D;
+    }
+    if (a.Nq == 1) decode_stream<T, D, 1>(a, S, st);
+    else if (a.Nq == 2) decode_stream<T, D, 2>(a, S, st);
+    else decode_stream<T, D, 4>(a, S, st);
+    int rc = gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_decode launch");
+    if (rc != 0 || S == 1) return rc;
+    const long long threads = (long long)a.B * a.H * a.Nq * (D / 8);
+    hipLaunchKernelGGL((gr_attn_combine_kernel<T, D>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                       a.part_o, a.part_ml, static_cast<T*>(a.o), a.o_sb, a.o_sh, a.o_sn, a.B, a.H, a.Nq, S,
+                       a.scale_log2);
+    return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_decode combine launch");
+  }
   const int nw = a.Nq <= 32 ? 1 : a.Nq <= 64 ? 2 : 4;
   const long long nqt = (a.Nq + 32 * nw - 1) / (32 * nw);
   const bool bn64 = a.N % 64 == 0;

@@ -205,8 +205,13 @@ def flash_attention(q, k, v, *, causal: bool = False, scale: float | None = None
 
 
 def decode_splits(B: int, H: int, Nq: int, N: int, cu_count: int = 256) -> int:
-    """Key parts per query tile for gr_attn_decode: enough workgroups for
-    two per compute unit, each part keeping at least four 64-key tiles."""
+    """Key parts per query tile for gr_attn_decode. Up to 4 queries (the
+    streaming kernel, 4 waves per workgroup): one workgroup per compute unit,
+    each part keeping at least 512 keys. More (the flash body): enough
+    workgroups for two per compute unit, each part keeping at least four
+    64-key tiles."""
+    if Nq <= 4:
+        return max(1, min(-(-cu_count // (B * H)), N // 512))
     nw = 1 if Nq <= 32 else 2 if Nq <= 64 else 4
     tiles_q = B * H * -(-Nq // (32 * nw))
     want = -(-2 * cu_count // tiles_q)

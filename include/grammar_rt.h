@@ -147,8 +147,11 @@ int gr_attn_bwd(const void* q, const void* k, const void* v, const void* o, cons
  *  Q, O: [B, H, Nq, D]; K, V: [B, H, N, D]; strides {batch, head, seq} in
  *  elements (multiples of 8), unit stride along D. N a multiple of 32; D in
  *  {64, 128}; dtype GR_F16 or GR_BF16.
- *  splits: workgroups per query tile that share out the keys (clamped to
- *  the number of 64- or 32-key tiles); with more than one, the partials go
+ *  Up to 4 queries run on a streaming kernel (K and V read once straight
+ *  into registers, scores on the VALU); more on the flash body's MFMA tiles.
+ *  splits: workgroups per head (up to 4 queries) or per query tile that
+ *  share out the keys (clamped to N/32, or to the number of 64- or 32-key
+ *  tiles); with more than one, the partials go
  *  through `workspace` (device memory of at least
  *  gr_attn_decode_workspace(B, H, Nq, D, splits) bytes, 16-byte aligned;
  *  the call then overwrites it) and a second kernel merges them. */

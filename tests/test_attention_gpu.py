@@ -178,6 +178,12 @@ DECODE = [
     (1, 2, 33, 96, 64, "fp16", 2),           # 96 keys: 32-key tiles
     (4, 16, 1, 8192, 128, "bf16", 0),
     (4, 2, 1024, 1024, 64, "fp16", 4),       # C2 at 8 heads, keys split four ways
+    # up to 4 queries: the streaming kernel
+    (1, 3, 2, 160, 64, "bf16", 1),           # one part, keys past the last full iteration
+    (2, 2, 3, 96, 128, "fp16", 2),           # 3 queries on the 4-query kernel
+    (1, 2, 4, 4096, 64, "fp16", 0),
+    (3, 1, 1, 32, 128, "bf16", 0),           # a single 32-key part
+    (1, 1, 1, 8192, 64, "fp16", 64),         # many parts
 ]
 
 
