@@ -310,6 +310,37 @@ def test_backward_parity(case):
         assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL, (name, mx, mn)
 
 
+def test_bound_training_launchers_repeat_and_validate():
+    """bind_flash_attention_train / bind_flash_attention_bwd: repeated launches
+    give bit-identical results (no state carried between calls, delta is
+    rewritten each time), and malformed operands are rejected before any
+    launch."""
+    dev = _cuda()
+    from grammar.attention import bind_flash_attention_bwd, bind_flash_attention_train
+    g = torch.Generator("cpu").manual_seed(15)
+    q, k, v, do = (torch.randn((2, 2, 512, 128), generator=g).to(torch.bfloat16).to(dev) for _ in range(4))
+    fwd, o, lse = bind_flash_attention_train(q, k, v, causal=True)
+    fwd()
+    bwd, grads = bind_flash_attention_bwd(q, k, v, o, do, lse, causal=True)
+    bwd()
+    torch.cuda.synchronize()
+    first = [t.clone() for t in (o, lse, *grads)]
+    fwd()
+    bwd()
+    torch.cuda.synchronize()
+    for a, b in zip(first, (o, lse, *grads)):
+        assert torch.equal(a, b)
+    with pytest.raises(ValueError):
+        bind_flash_attention_bwd(q, k, v, o, do.transpose(2, 3), lse)            # not [B, H, N, D]
+    with pytest.raises(ValueError):
+        bind_flash_attention_bwd(q, k, v, o, do[:, :, ::2].repeat(1, 1, 2, 1).transpose(1, 2).contiguous()
+                                 .transpose(1, 2), lse)                           # non-contiguous
+    with pytest.raises(ValueError):
+        bind_flash_attention_bwd(q, k, v, o, do, lse.half())                       # lse must be fp32
+    with pytest.raises(ValueError):
+        bind_flash_attention_bwd(q, k, v, o, do, lse, workspace=torch.empty(16, dtype=torch.uint8, device=dev))
+
+
 def test_autograd_training_step_matches_oracle():
     """flash_attention as a torch.autograd function: loss.backward() gives the
     oracle's gradients."""
