@@ -12,17 +12,18 @@
 //  * Scores are dot products on the VALU in fp32 (the query pre-scaled into
 //    exponent units, c = scale log2(e)), reduced across a row's lanes by
 //    shuffles; the online softmax runs per iteration of 64/(D/8)*U keys.
-//  * A workgroup (4 waves) takes one head and one part of the keys (grid.y =
-//    key parts); its waves take consecutive quarters of the part and merge
+//  * A workgroup (NWV waves) takes one head and one part of the keys (grid.y
+//    = key parts); its waves take consecutive slices of the part and merge
 //    through LDS. With more than one part each writes its unnormalised O and
 //    (max, row sum) and gr_attn_combine_kernel merges them, as for the flash
 //    body's key split.
 #pragma once
 #include "gr_flash_fwd.h"
 
-template <class T, int D, int NQ, int U>
-__global__ __launch_bounds__(256) void gr_attn_decode_stream_kernel(gr_attn_args a) {
-  constexpr int NWV = 4;            // waves per workgroup
+// NWV waves per workgroup, NQ >= a.Nq query slots, U key-row loads of K and
+// of V per lane and iteration.
+template <class T, int D, int NQ, int U, int NWV>
+__device__ __forceinline__ void gr_attn_decode_stream_body(const gr_attn_args& a) {
   constexpr int LPK = D / 8;        // lanes per key row
   constexpr int KPR = 64 / LPK;     // key rows per wave load
   constexpr int KPI = KPR * U;      // keys per wave iteration
@@ -52,7 +53,7 @@ __global__ __launch_bounds__(256) void gr_attn_decode_stream_kernel(gr_attn_args
     l[qi] = 0.f;
   }
 
-  // this wave's keys: a quarter of the part, a whole number of iterations
+  // this wave's keys: a 1/NWV slice of the part, a whole number of iterations
   const int per = ((kend - key0 + NWV * KPI - 1) / (NWV * KPI)) * KPI;
   const int kw0 = key0 + wave * per;
   const int kw1 = gr_imin(kend, kw0 + per);
@@ -164,4 +165,9 @@ __global__ __launch_bounds__(256) void gr_attn_decode_stream_kernel(gr_attn_args
     *reinterpret_cast<gr_f32x4*>(po + 4) = (gr_f32x4){acc[4], acc[5], acc[6], acc[7]};
     if (c8 == 0) *reinterpret_cast<gr_f32x2*>(a.part_ml + part * 2) = (gr_f32x2){M / c, L};
   }
+}
+
+template <class T, int D, int NQ, int U, int NWV = 4>
+__global__ __launch_bounds__(NWV * 64) void gr_attn_decode_stream_kernel(gr_attn_args a) {
+  gr_attn_decode_stream_body<T, D, NQ, U, NWV>(a);
 }
