@@ -4,11 +4,12 @@
 // the forward's row log-sum-exp L (natural log of sum_j exp(scale q.k_j)),
 // computes dV = P^T dO, dK = scale dS^T Q, dQ = scale dS K with
 // P = exp(scale Q K^T - L) [causal mask], dS = P * (dO V^T - delta),
-// delta = rowsum(dO * O). Three kernels:
+// delta = rowsum(dO * O). Two kernels (the dQ one runs first):
 //  * gr_attn_bwd_kernel (dK, dV): one workgroup per block of BN keys of one
-//    head, one wave per 32 of them. K and V of the wave stay in registers as
-//    MFMA operands; dK^T and dV^T accumulate in registers over all query
-//    tiles. Per tile of BM queries (Q and dO double-buffered in LDS, loaded
+//    head, one wave per 32 of them. K and V of the wave are MFMA operands
+//    held in registers (d = 64) or read per use from the wave's rows in LDS
+//    (d = 128, gr_attn_bwd_lds::KV_LDS); dK^T and dV^T accumulate in
+//    registers over all query tiles. Per tile of BM queries (Q and dO double-buffered in LDS, loaded
 //    straight from global memory): S = Q K^T and dP = dO V^T with one key per
 //    lane (Q and dO rows read with bits 2 and 3 of the row index swapped, so
 //    each half-wave's accumulators hold 8 consecutive queries: they are
@@ -24,7 +25,8 @@
 //    the dO fragments it holds, storing it for the dK/dV kernel.
 // Causal: a key block meets only the query tiles at or after its first key
 // (and a query tile only the key tiles up to its last query); the mask is
-// applied on the tiles that straddle the diagonal.
+// applied on the 32-row blocks that straddle the diagonal. Outputs are staged
+// through the free LDS and stored as whole rows (gr_store_block_t).
 #pragma once
 #include "gr_flash_fwd.h"
 
