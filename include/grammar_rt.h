@@ -101,7 +101,10 @@ int gr_plan_time(gr_plan* p, void* stream, int warmup, int iters, int mode, floa
  * Replaces the attention module contract fn(KT, Q, V) (bench.py:14-20,
  * pytorch-naive.py:23-65, grammar/kernel_ast.py:1267-1287) and the SDPA
  * reference point (flash-attn2-sota.py:41-62).
- *  dtype: GR_F16 or GR_BF16 (fp32 accumulate).
+ *  dtype: GR_F16 or GR_BF16 (fp32 accumulate). With GR_F16 the kernel
+ *  rounds Q * scale * log2(e) to fp16 once (the scores then need no per-score
+ *  scaling), so |q| * scale * log2(e) must stay below 65504: always so when
+ *  scale * log2(e) <= 1, as for the default 1/sqrt(D) with D >= 3.
  *  Q, V, O: [B, H, N, D] with strides {batch, head, seq} in elements
  *  (unit stride along D). K: [B, H, N, D] if k_transposed == 0, else KT
  *  [B, H, D, N] whose k_strides = {batch, head, d} (unit stride along N).
