@@ -11,7 +11,7 @@ config C2), with the descent's evals/min measured in the same run.
    most S seconds; every variant is rendered to HIP, compiled with hiprtc,
    checked against the fp32 closed form and timed. evals/min = timed variants
    per wall minute. With S = 0 the committed best program of an earlier
-   descent (runs/attn_c2_best.json) is used instead.
+   descent (runs/attn_c2_best.json, or attn_c3_best.json with --config C3) is used instead.
 2. Timing: a "step" is one forward of the descent's best program over the
    whole batch, inputs resident in HBM. W untimed warmup steps, then exactly
    K steps between two hipEvents recorded on the stream the kernels run on,
@@ -42,7 +42,9 @@ sys.path.insert(0, REPO)
 
 METRIC = "attn fwd TFLOP/s, % fp16 MFMA peak (B4 H16 N1024 d64); descent evals/min"
 PEAK_TFLOPS = {"fp16": 2500.0, "bf16": 2500.0}     # MI355X dense MFMA, published
-BEST_PROGRAM = os.path.join(PKG, "runs", "attn_c2_best.json")
+def best_program_path(config: str) -> str:
+    """The committed best program of an earlier descent for C2 or C3."""
+    return os.path.join(PKG, "runs", f"attn_{config.lower()}_best.json")
 
 
 def log(*a):
@@ -363,8 +365,10 @@ def main() -> int:
     ap.add_argument("--no-side", action="store_true",
                     help="skip the committed descent-found C3 / C4 programs, the torch SDPA reference point, "
                          "the training (forward + backward) timings and the one-GPU-share shapes")
-    ap.add_argument("--block-m", type=int, default=256, help="hand-written kernel: queries per workgroup")
-    ap.add_argument("--block-n", type=int, default=128, help="hand-written kernel: keys per tile")
+    ap.add_argument("--block-m", type=int, default=None,
+                    help="hand-written kernel: queries per workgroup (default 256 at d = 64, else the library's choice)")
+    ap.add_argument("--block-n", type=int, default=None,
+                    help="hand-written kernel: keys per tile (default 128 at d = 64, else the library's choice)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run --steps plain device copies of MIB MiB "
                          "(the known-size reference that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -395,6 +399,10 @@ def main() -> int:
 
     cfg = CONFIGS[args.config]
     peak = PEAK_TFLOPS[cfg.dtype]
+    if args.block_m is None:
+        args.block_m = 256 if cfg.D == 64 else 0
+    if args.block_n is None:
+        args.block_n = 128 if cfg.D == 64 else 0
     q, k, v = (t.to(dev) for t in attention_inputs(cfg, seed=args.seed))
     kt = k.transpose(-1, -2).contiguous()
 
@@ -408,10 +416,11 @@ def main() -> int:
             best, search = run_descent(cfg, args.search_seconds, args.seed)
             log(f"[bench] descent: {search}")
         else:
-            with open(BEST_PROGRAM) as f:
+            best_path = best_program_path(cfg.name)
+            with open(best_path) as f:
                 saved = json.load(f)
             best = program_from_key(saved["key"])
-            search = {"source": os.path.relpath(BEST_PROGRAM, REPO), "evals_per_min": saved.get("evals_per_min")}
+            search = {"source": os.path.relpath(best_path, REPO), "evals_per_min": saved.get("evals_per_min")}
         mod = HipModule(emit_module(best))
         tensors = {"Q": q, "KT": kt, "V": v}
         tensors.update(mod.allocate(dev))

@@ -70,3 +70,11 @@ def test_best_so_far_curve_keeps_improvements_only():
     assert [p[1] for p in curve] == [1, 4]          # variant index of each improvement
     assert [p[2] for p in curve] == [0.3, 0.1]      # best ms, strictly decreasing
     assert curve[-1][3] == round(1e12 / 0.1e-3 / 1e12, 1)
+
+
+def test_committed_best_program_per_config():
+    sys.path.insert(0, REPO)
+    import bench
+    for cfg in ("C2", "C3"):
+        path = bench.best_program_path(cfg)
+        assert os.path.basename(path) == f"attn_{cfg.lower()}_best.json" and os.path.exists(path)
