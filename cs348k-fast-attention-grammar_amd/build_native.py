@@ -1,8 +1,13 @@
-"""Build libgrammar_rt.so (the C-ABI runtime + hand-written gfx950 kernels).
+"""Build libgrammar_rt.so (the C-ABI runtime + hand-written gfx950 kernels)
+and libgrammar_rtc.so (the hiprtc compile entry points alone).
 
-Every source under csrc/ is compiled with hipcc for gfx950 only, with packed
-FP32 instructions disabled, into lib/libgrammar_rt.so next to this file. The
-objects are compiled in parallel; the link is one hipcc call.
+Every .hip / .cpp source under csrc/ is compiled with hipcc for gfx950 only,
+with packed FP32 instructions disabled, and linked into lib/libgrammar_rt.so
+next to this file. gr_rtc.cpp (hiprtc compilation and the error slot, no HIP
+runtime call) is host C++ built with g++; it is linked into libgrammar_rt.so
+and, on its own, into lib/libgrammar_rtc.so, the library the compile worker
+processes load (they never open the GPU). The objects are compiled in
+parallel.
 
     python build_native.py            # build (always recompiles)
 """
@@ -20,7 +25,11 @@ CSRC = os.path.join(HERE, "csrc")
 LIBDIR = os.path.join(HERE, "lib")
 OBJDIR = os.path.join(HERE, "lib", "obj")
 LIB = os.path.join(LIBDIR, "libgrammar_rt.so")
+RTC_LIB = os.path.join(LIBDIR, "libgrammar_rtc.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CXX = os.environ.get("CXX", "g++")
+ROCM = "/opt/rocm"
+HOST_ONLY = ("gr_rtc.cpp",)   # host C++ (hiprtc only), built with CXX
 
 COMMON = [
     "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",
@@ -45,9 +54,13 @@ def _sources() -> list[str]:
 
 def _compile(src: str) -> str:
     obj = os.path.join(OBJDIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *COMMON, *EXTRA.get(os.path.basename(src), []), "-c", src, "-o", obj]
-    if src.endswith(".cpp"):
-        cmd[1:1] = ["-x", "hip"]
+    if os.path.basename(src) in HOST_ONLY:
+        cmd = [CXX, "-O2", "-std=c++17", "-fPIC", "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROCM, "include"),
+               "-I", CSRC, "-I", os.path.join(REPO, "include"), "-c", src, "-o", obj]
+    else:
+        cmd = [HIPCC, *COMMON, *EXTRA.get(os.path.basename(src), []), "-c", src, "-o", obj]
+        if src.endswith(".cpp"):
+            cmd[1:1] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
@@ -61,15 +74,18 @@ def build(verbose: bool = True) -> str:
     jobs = min(len(srcs), int(os.environ.get("MAX_JOBS", "8")))
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         objs = list(ex.map(_compile, srcs))
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", *objs, "-o", tmp,
-           "-L/opt/rocm/lib", "-lhiprtc", "-Wl,-rpath,/opt/rocm/lib"]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
+    rtc_objs = [o for o in objs if os.path.basename(o)[:-2] in HOST_ONLY]
+    links = ((LIB, [HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", *objs]),
+             (RTC_LIB, [CXX, "-shared", "-fPIC", *rtc_objs]))
+    for out, cmd in links:
+        tmp = out + ".tmp"
+        r = subprocess.run(cmd + ["-o", tmp, f"-L{ROCM}/lib", "-lhiprtc", f"-Wl,-rpath,{ROCM}/lib"],
+                           capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"link of {out} failed:\n{r.stdout}\n{r.stderr}")
+        os.replace(tmp, out)
     if verbose:
-        print(f"[build_native] {LIB} ({len(srcs)} sources, {time.time() - t0:.1f}s)", flush=True)
+        print(f"[build_native] {LIB}, {RTC_LIB} ({len(srcs)} sources, {time.time() - t0:.1f}s)", flush=True)
     return LIB
 
 

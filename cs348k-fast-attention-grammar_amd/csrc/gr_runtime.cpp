@@ -1,12 +1,12 @@
-// gr_runtime.cpp -- hiprtc compilation, code-object loading, launch plans and
-// hipEvent timing behind the C ABI in include/grammar_rt.h.
+// gr_runtime.cpp -- code-object loading, launch plans and hipEvent timing
+// behind the C ABI in include/grammar_rt.h (hiprtc compilation and the error
+// slot live in gr_rtc.cpp).
 //
-// This is the MI355X replacement for the part of the reference that cuTile and
-// cupy provide: JIT compile of the emitted module (grammar/optimization.py:
-// 262-283), ct.launch of each stage (grammar/kernel_ast.py:1268-1276) and the
-// cp.cuda.Event timing loops (grammar/optimization.py:284-300, bench.py:49-74).
+// This is the MI355X replacement for the part of the reference that cupy
+// provides: loading the JIT-compiled module, ct.launch of each stage
+// (grammar/kernel_ast.py:1268-1276) and the cp.cuda.Event timing loops
+// (grammar/optimization.py:284-300, bench.py:49-74).
 #include <hip/hip_runtime.h>
-#include <hip/hiprtc.h>
 
 #include <cstdlib>
 #include <cstring>
@@ -17,18 +17,6 @@
 #include "grammar_rt.h"
 
 namespace gr {
-
-static thread_local std::string g_err;
-
-int fail(int code, const char* fmt, ...) {
-  char buf[2048];
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(buf, sizeof(buf), fmt, ap);
-  va_end(ap);
-  g_err = buf;
-  return code;
-}
 
 int hip_check(hipError_t e, int code, const char* what) {
   if (e == hipSuccess) return GR_OK;
@@ -61,18 +49,6 @@ struct gr_plan {
 
 extern "C" {
 
-const char* gr_last_error(void) { return gr::g_err.c_str(); }
-
-const char* gr_version(void) {
-  static std::string v;
-  if (v.empty()) {
-    int maj = 0, min = 0;
-    hiprtcVersion(&maj, &min);
-    v = "gfx950 hiprtc " + std::to_string(maj) + "." + std::to_string(min);
-  }
-  return v.c_str();
-}
-
 int gr_device_info(int device, long long* out5) {
   if (!out5) return gr::fail(GR_E_ARG, "gr_device_info: null output");
   hipDeviceProp_t p;
@@ -85,52 +61,6 @@ int gr_device_info(int device, long long* out5) {
   out5[4] = p.l2CacheSize;
   return GR_OK;
 }
-
-int gr_compile(const char* src, const char* name, const char* const* opts, int nopts, void** code,
-               size_t* code_size, char* log, size_t loglen) {
-  if (!src || !code || !code_size) return gr::fail(GR_E_ARG, "gr_compile: null argument");
-  if (log && loglen) log[0] = 0;
-  hiprtcProgram prog;
-  hiprtcResult r = hiprtcCreateProgram(&prog, src, name ? name : "gr_module.hip", 0, nullptr, nullptr);
-  if (r != HIPRTC_SUCCESS) return gr::fail(GR_E_COMPILE, "hiprtcCreateProgram: %s", hiprtcGetErrorString(r));
-  std::vector<const char*> o;
-  o.push_back("--offload-arch=gfx950");
-  o.push_back("-O3");
-  o.push_back("-std=c++17");
-  // Packed FP32 instructions stay disabled in every kernel this library builds.
-  o.push_back("-Xclang");
-  o.push_back("-target-feature");
-  o.push_back("-Xclang");
-  o.push_back("-packed-fp32-ops");
-  for (int i = 0; i < nopts; ++i) o.push_back(opts[i]);
-  r = hiprtcCompileProgram(prog, (int)o.size(), o.data());
-  if (r != HIPRTC_SUCCESS) {
-    size_t ls = 0;
-    hiprtcGetProgramLogSize(prog, &ls);
-    std::string lg(ls + 1, '\0');
-    if (ls) hiprtcGetProgramLog(prog, &lg[0]);
-    if (log && loglen) {
-      strncpy(log, lg.c_str(), loglen - 1);
-      log[loglen - 1] = 0;
-    }
-    hiprtcDestroyProgram(&prog);
-    return gr::fail(GR_E_COMPILE, "hiprtc compile failed: %.1500s", lg.c_str());
-  }
-  size_t cs = 0;
-  hiprtcGetCodeSize(prog, &cs);
-  void* buf = malloc(cs);
-  if (!buf) {
-    hiprtcDestroyProgram(&prog);
-    return gr::fail(GR_E_RUNTIME, "gr_compile: out of host memory");
-  }
-  hiprtcGetCode(prog, (char*)buf);
-  hiprtcDestroyProgram(&prog);
-  *code = buf;
-  *code_size = cs;
-  return GR_OK;
-}
-
-void gr_free_code(void* code) { free(code); }
 
 int gr_module_load(const void* code, size_t code_size, gr_module** out) {
   if (!code || !code_size || !out) return gr::fail(GR_E_ARG, "gr_module_load: null argument");

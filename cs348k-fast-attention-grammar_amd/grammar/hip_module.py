@@ -6,9 +6,13 @@ contract fn(*inputs) + KERNEL_META, bench.py:14-20).
     out = mod.fn(*inputs)                   # inputs in sorted-name order
     ms = mod.time(inputs, warmup, iters)    # hipEvents around the launch plan
 
-Compilation goes through hiprtc (runtime.compile_source) with an in-process
-cache and an on-disk code-object cache keyed by (source hash, toolchain
-version). Intermediates and outputs are allocated once per bound input set
+Compilation goes through hiprtc (runtime.compile_source, or a CompilePool of
+worker processes) with an in-process cache and an on-disk code-object cache.
+The cache key covers everything the code object depends on: the rendered
+source, the hiprtc version, the compile options and the bytes of every header
+the source can include (csrc/*.h, pulled in through -I csrc), so an edited
+header never reaches a kernel through a stale code object. Intermediates and
+outputs are allocated once per bound input set
 (the reference reallocates them with cp.zeros on every call,
 kernel_ast.py:1271-1272); they start NaN-filled so an incomplete write shows.
 """
@@ -32,41 +36,79 @@ def cache_dir() -> str | None:
     return d
 
 
+_toolchain = None
+
+
+def toolchain_digest() -> str:
+    """Digest of what a rendered module's code object depends on besides its
+    own text: hiprtc's version, the fixed compile options (set in
+    csrc/gr_rtc.cpp) and every header under csrc/. Computed once per process."""
+    global _toolchain
+    if _toolchain is None:
+        h = hashlib.sha256()
+        h.update(rt.version().encode())
+        for name in sorted(os.listdir(rt.CSRC_DIR)):
+            if name.endswith(".h") or name == "gr_rtc.cpp":
+                h.update(b"\0" + name.encode() + b"\0")
+                with open(os.path.join(rt.CSRC_DIR, name), "rb") as f:
+                    h.update(f.read())
+        _toolchain = h.hexdigest()
+    return _toolchain
+
+
 def source_key(src: str) -> str:
     h = hashlib.sha256()
-    h.update(rt.version().encode())
+    h.update(toolchain_digest().encode())
     h.update(b"\0")
     h.update(src.encode())
     return h.hexdigest()[:32]
 
 
-def compile_cached(src: str, name: str = "gr_module.hip") -> tuple:
-    """(code object bytes, cache hit?) for `src`."""
+def _cache_path(key: str) -> str | None:
+    d = cache_dir()
+    return os.path.join(d, key + ".co") if d else None
+
+
+def lookup_cached(src: str) -> bytes | None:
+    """The code object of `src` from the in-process or on-disk cache, or None."""
     key = source_key(src)
     with _lock:
         code = _mem_cache.get(key)
     if code is not None:
-        return code, True
-    d = cache_dir()
-    path = os.path.join(d, key + ".co") if d else None
+        return code
+    path = _cache_path(key)
     if path and os.path.exists(path):
         with open(path, "rb") as f:
             code = f.read()
         with _lock:
             _mem_cache[key] = code
-        return code, True
-    code = rt.compile_source(src, name)
+        return code
+    return None
+
+
+def store_cached(src: str, code: bytes) -> None:
+    key = source_key(src)
     with _lock:
         _mem_cache[key] = code
+    path = _cache_path(key)
     if path:
         try:
-            os.makedirs(d, exist_ok=True)
-            tmp = f"{path}.{os.getpid()}.tmp"
+            os.makedirs(os.path.dirname(path), exist_ok=True)
+            tmp = f"{path}.{os.getpid()}.{threading.get_ident()}.tmp"
             with open(tmp, "wb") as f:
                 f.write(code)
             os.replace(tmp, path)
         except OSError:
             pass
+
+
+def compile_cached(src: str, name: str = "gr_module.hip") -> tuple:
+    """(code object bytes, cache hit?) for `src`, compiled in this process on a miss."""
+    code = lookup_cached(src)
+    if code is not None:
+        return code, True
+    code = rt.compile_source(src, name)
+    store_cached(src, code)
     return code, False
 
 

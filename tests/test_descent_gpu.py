@@ -1,0 +1,153 @@
+"""GPU parity of what the benchmark times: the committed descent-found
+programs for C2, C3 and C4 rendered by the HIP backend and run at their full
+configs against the CPU oracle, and the live descent loop (render -> hiprtc
+compile -> tolerance check -> hipEvent timing) on a small attention problem,
+including a variant the checker must reject.
+
+Reference behaviour pinned: the descent loss and its scores
+(grammar/optimization.py:251-300), the final `verify` of the best program
+(run_attention_search.py:169-181), the MLP block (run_mlp_search.py:42-127).
+Tolerance: max-abs <= 2e-2, mean-abs <= 2e-3 against the fp32 CPU oracle on
+the same rounded inputs."""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import PKG
+from oracle import attention as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _cuda():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    return torch.device("cuda:0")
+
+
+def _case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _load(name):
+    from grammar.kernel_ast import program_from_key
+    with open(os.path.join(PKG, "runs", name)) as f:
+        saved = json.load(f)
+    return program_from_key(saved["key"]), saved
+
+
+def _check(got, ref, what):
+    got = got.float().cpu().numpy() if isinstance(got, torch.Tensor) else got
+    mx, mn = O.errors(got, ref)
+    print(f"[check] {what}: max-abs {mx:.3e} mean-abs {mn:.3e}", flush=True)
+    assert np.isfinite(mx) and mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL, (what, mx, mn)
+
+
+def test_committed_c2_program_full_config_vs_oracle():
+    dev = _cuda()
+    from grammar.hip_module import HipModule
+    from grammar.kernel_ast import emit_module
+    from grammar.workloads import C2, attention_inputs
+    prog, saved = _load("attn_c2_best.json")
+    _case(f"committed C2 program {saved['stages']}")
+    mod = HipModule(emit_module(prog))
+    assert [s["lowering"] for s in mod.plan["steps"]] == ["flash"]
+    q, k, v = attention_inputs(C2, seed=0)
+    kt = k.transpose(-1, -2).contiguous()
+    out = mod.fn(kt.to(dev), q.to(dev), v.to(dev))
+    torch.cuda.synchronize()
+    ref = O.attention(q.float().numpy(), kt.float().numpy(), v.float().numpy(), k_transposed=True)
+    _check(out, ref, "C2 descent program (all 64 heads)")
+    again = mod.fn(kt.to(dev), q.to(dev), v.to(dev))
+    assert torch.equal(out, again), "descent-found C2 kernel is not deterministic"
+
+
+def test_committed_c3_program_sampled_heads_vs_oracle():
+    dev = _cuda()
+    from grammar.hip_module import HipModule
+    from grammar.kernel_ast import emit_module
+    from grammar.workloads import C3, attention_inputs
+    prog, saved = _load("attn_c3_best.json")
+    _case(f"committed C3 program {saved['stages']}")
+    mod = HipModule(emit_module(prog))
+    q, k, v = attention_inputs(C3, seed=0)
+    kt = k.transpose(-1, -2).contiguous()
+    out = mod.fn(kt.to(dev), q.to(dev), v.to(dev)).float().cpu()
+    assert torch.isfinite(out).all()
+    for b, h in ((0, 0), (1, 31), (0, 17)):
+        ref = O.attention(q[b, h].float().numpy(), k[b, h].float().numpy(), v[b, h].float().numpy(), causal=True)
+        _check(out[b, h], ref, f"C3 descent program head ({b},{h})")
+
+
+def test_committed_c4_program_sampled_rows_vs_oracle():
+    dev = _cuda()
+    from grammar.hip_module import HipModule
+    from grammar.kernel_ast import emit_module
+    from grammar.workloads import C4, mlp_inputs
+    prog, saved = _load("mlp_c4_best.json")
+    _case(f"committed C4 program {saved['stages']}")
+    mod = HipModule(emit_module(prog))
+    x, w1, w2 = mlp_inputs(C4, seed=0)
+    named = {"X": x.to(dev), "W1": w1.to(dev), "W2": w2.to(dev)}
+    y = mod.fn(*[named[n] for n in mod.inputs])
+    torch.cuda.synchronize()
+    rows = np.random.default_rng(3).choice(C4.M, 192, replace=False)
+    ref = O.mlp_silu(x[rows].float().numpy(), w1.float().numpy(), w2.float().numpy(), dtype=np.float32)
+    _check(y[torch.as_tensor(rows, device=dev)], ref, "C4 descent program rows")
+
+
+def _small_attention():
+    import run_attention_search as RS
+    return RS.build_attention(256, 64, B=1, H=2, dtype="fp16"), RS.attention_reference(1.0 / math.sqrt(64))
+
+
+def test_live_descent_finds_a_kernel_that_passes_the_oracle(tmp_path, monkeypatch):
+    dev = _cuda()
+    monkeypatch.setenv("GR_CACHE_DIR", str(tmp_path / "co"))
+    from grammar.hip_module import HipModule
+    from grammar.kernel_ast import emit_module, kernel_meta
+    from grammar.optimization import EvalConfig, Evaluator, SearchConfig, autotune
+    prog, ref = _small_attention()
+    _case("live descent B1 H2 N256 d64 fp16, 8 iterations")
+    ev = Evaluator(EvalConfig(seed=0), reference=ref)
+    try:
+        best = autotune(prog, ev, SearchConfig(iters=8, N=2, K=4, seed=0, verbose=False, time_budget_s=60))
+        st = ev.stats()
+        print(f"[descent] {st}", flush=True)
+        assert st["timed_variants"] > 0 and st["hiprtc_compiles"] > 0
+        assert ev(best) < 1e9
+        assert len(ev.timeline) == st["timed_variants"]
+        # the best program against the CPU oracle on fresh seeded inputs
+        g = torch.Generator("cpu").manual_seed(11)
+        ins = {n: torch.randn(tuple(s), generator=g).half() for n, s in kernel_meta(best)["inputs"]}
+        mod = HipModule(emit_module(best))
+        out = mod.fn(*[ins[n].to(dev) for n in mod.inputs])
+        torch.cuda.synchronize()
+        oref = O.attention(ins["Q"].float().numpy(), ins["KT"].float().numpy(), ins["V"].float().numpy(),
+                           k_transposed=True)
+        _check(out, oref, "live descent best")
+    finally:
+        ev.close()
+
+
+def test_evaluator_rejects_a_variant_that_fails_the_checker(tmp_path, monkeypatch):
+    _cuda()
+    monkeypatch.setenv("GR_CACHE_DIR", str(tmp_path / "co"))
+    from grammar.optimization import EvalConfig, Evaluator
+    prog, ref = _small_attention()
+    _case("evaluator: correct vs deliberately wrong reference")
+    good = Evaluator(EvalConfig(seed=0), reference=ref)
+    bad = Evaluator(EvalConfig(seed=0), reference=lambda named: ref(named) * 1.5 + 0.25)
+    try:
+        loss = good(prog)
+        assert 0 < loss < 1e9 and good.stats()["timed_variants"] == 1
+        assert bad(prog) == math.inf
+        assert bad.stats()["timed_variants"] == 0     # never timed
+        assert len(bad.timeline) == 0
+    finally:
+        good.close()
+        bad.close()

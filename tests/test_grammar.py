@@ -65,7 +65,7 @@ def test_flops_invariant_under_tiling_and_subtile():
 
 
 def _loads(prog):
-    return [s for l in prog.body for s in R._all_stmts(l.body) if isinstance(s, Load)]
+    return [s for l in prog.body for s in R.statements(l.body) if isinstance(s, Load)]
 
 
 def _build_red():
@@ -350,7 +350,7 @@ def test_hoist_compute_inverts_sink_compute():
     S = next(s for s in rl.body if isinstance(s, Compute) and s.op == "matmul")
     assert not R.can_hoist_compute(q, S)[0]       # reads KT loaded inside the loop
     q1 = R.hoist(q, kt)
-    S1 = next(s for s in R._all_stmts(q1.body[0].body) if isinstance(s, Compute) and s.op == "matmul")
+    S1 = next(s for s in R.statements(q1.body[0].body) if isinstance(s, Compute) and s.op == "matmul")
     assert R.can_hoist_compute(q1, S1)[0]
     q2 = R.hoist_compute(q1, S1)
     assert np.allclose(_run(q2)[0], r0, rtol=1e-3, atol=1e-3)

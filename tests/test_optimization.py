@@ -67,7 +67,6 @@ def test_rewrite_descriptor_reresolves_on_clone():
     p = C.p_matmul_full_k()
     rw = next(r for r in O.enumerate_rewrites(p, ("subtile_reduction",)))
     q = R.clone_program(p)
-    R._strip_clone_meta(q)
     out = rw.resolve(q)
     assert out is not None and any(isinstance(s, ReductionLoop) for s in out.body[0].body)
 

@@ -31,7 +31,7 @@ def test_plan_matches_kernel_meta():
 
 
 def _loads(p):
-    return [s for l in p.body for s in R._all_stmts(l.body) if isinstance(s, Load)]
+    return [s for l in p.body for s in R.statements(l.body) if isinstance(s, Load)]
 
 
 def test_hoist_emits_subtile_reads_and_sink_removes_them():

@@ -54,7 +54,7 @@ def test_rewrites_preserve_results_on_gpu():
     base, _ = _gpu_run(p, ins)
     h = p
     for src in ("x", "y"):
-        ld = [s for l in h.body for s in R._all_stmts(l.body) if isinstance(s, Load) and s.source == src][0]
+        ld = [s for l in h.body for s in R.statements(l.body) if isinstance(s, Load) and s.source == src][0]
         h = R.hoist(h, ld)
     assert "GR_SUBTILE" in emit_module(h)
     assert np.allclose(_gpu_run(h, ins)[0], base, rtol=1e-3, atol=1e-3)
