@@ -40,7 +40,12 @@ PKG = os.path.join(REPO, "cs348k-fast-attention-grammar_amd")
 sys.path.insert(0, PKG)
 sys.path.insert(0, REPO)
 
-METRIC = "attn fwd TFLOP/s, % fp16 MFMA peak (B4 H16 N1024 d64); descent evals/min"
+def metric_for(cfg) -> str:
+    """BASELINE.json's metric string, for the attention config being timed."""
+    return (f"attn fwd TFLOP/s, % {cfg.dtype} MFMA peak (B{cfg.B} H{cfg.H} N{cfg.N} d{cfg.D}"
+            f"{' causal' if cfg.causal else ''}); descent evals/min")
+
+
 PEAK_TFLOPS = {"fp16": 2500.0, "bf16": 2500.0}     # MI355X dense MFMA, published
 def best_program_path(config: str) -> str:
     """The committed best program of an earlier descent for C2 or C3."""
@@ -97,20 +102,29 @@ def measured_traffic(key: str):
         return None
 
 
-def timed(step, steps: int, warmup: int, min_warm_s: float = 0.05) -> float:
-    """ms per step: `warmup` untimed calls (continued until the GPU has been
-    busy for at least min_warm_s: its clocks ramp up over the first tens of
-    milliseconds of load), then `steps` calls between two events on the
-    current stream, synchronized on both sides."""
+CLOCK_RAMP_MS = 50.0   # the GPU clocks ramp up over the first tens of milliseconds of load
+_ramps: list = []       # (label-free) ramp steps of every timed() call, for the JSON line
+
+
+def timed(step, steps: int, warmup: int, ramp_ms: float = CLOCK_RAMP_MS) -> float:
+    """ms per step, the same way for every leg: `warmup` untimed calls, then
+    further untimed calls until the GPU has been kept busy for `ramp_ms` of
+    wall time (its clocks ramp up over the first tens of milliseconds of
+    load; the count of these extra calls is recorded), then `steps` calls
+    between two events on the current stream, synchronized on both sides."""
     import torch
-    t0 = time.perf_counter()
-    n = 0
-    while n < warmup or time.perf_counter() - t0 < min_warm_s:
+    for _ in range(warmup):
         step()
-        n += 1
-        if n % 64 == 0 or n == warmup:
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    extra = 0
+    while (time.perf_counter() - t0) * 1e3 < ramp_ms:
+        step()
+        extra += 1
+        if extra % 64 == 0:
             torch.cuda.synchronize()
     torch.cuda.synchronize()
+    _ramps.append(extra)
     stream = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -317,23 +331,97 @@ def shard_shapes(steps: int, seed: int) -> dict:
 
 
 def run_descent(cfg, seconds: float, seed: int):
-    """The rewrite descent from the naive program for at most `seconds`."""
+    """The rewrite descent from the naive program for at most `seconds`
+    (500 iterations at most, C5), with a fresh, empty code-object cache so
+    every variant it times is compiled by hiprtc in this run or reuses the
+    code object of an identical source compiled earlier in it."""
+    import tempfile
     import run_attention_search as RS
     from grammar.optimization import Evaluator, EvalConfig, SearchConfig, autotune
     prog = RS.build_attention(cfg.N, cfg.D, B=cfg.B, H=cfg.H, dtype=cfg.dtype, causal=cfg.causal)
-    ev = Evaluator(EvalConfig(seed=seed), reference=RS.attention_reference(1.0 / math.sqrt(cfg.D), cfg.causal))
-    t0 = time.time()
-    best = autotune(prog, ev, SearchConfig(iters=500, N=4, K=5, seed=seed, verbose=False,
-                                            time_budget_s=seconds))
-    wall = time.time() - t0
-    st = ev.stats()
-    info = {"seconds": round(wall, 1), "timed_variants": st["timed_variants"],
-            "compiled_variants": st["compiled_variants"], "cache_hits": st["cache_hits"],
+    with tempfile.TemporaryDirectory(prefix="gr_bench_cache_") as cache:
+        old = os.environ.get("GR_CACHE_DIR")
+        os.environ["GR_CACHE_DIR"] = cache
+        try:
+            ev = Evaluator(EvalConfig(seed=seed), reference=RS.attention_reference(1.0 / math.sqrt(cfg.D), cfg.causal))
+            t0 = time.time()
+            best = autotune(prog, ev, SearchConfig(iters=500, N=4, K=5, seed=seed, verbose=False,
+                                                    time_budget_s=seconds))
+            wall = time.time() - t0
+            st = ev.stats()
+            best_loss = ev(best)
+            ev.close()
+        finally:
+            if old is None:
+                os.environ.pop("GR_CACHE_DIR", None)
+            else:
+                os.environ["GR_CACHE_DIR"] = old
+    info = {"seconds": round(wall, 1), "iterations": getattr(ev, "iterations", None), "iterations_max": 500,
+            "timed_variants": st["timed_variants"], "hiprtc_compiles": st["hiprtc_compiles"],
+            "code_cache_hits": st["code_cache_hits"], "memo_hits": st["memo_hits"],
+            "compile_timeouts": st["compile_timeouts"], "nondeterministic": st["nondeterministic"],
             "evals_per_min": round(60.0 * st["timed_variants"] / max(wall, 1e-9), 1),
-            "best_loss_ms": round(ev(best), 6), "start": "naive 8-stage program, full-extent tiles",
+            "evals_note": ("timed variants (compiled or code-cache hit, checked, timed) per wall minute; "
+                           "the code-object cache starts empty"),
+            "best_loss_ms": round(best_loss, 6), "start": "naive 8-stage program, full-extent tiles",
             "stages": [[l.out, list(l.tile_shape)] for l in best.body],
             "best_so_far": best_so_far(ev.timeline, cfg.flops)}
     return best, info
+
+
+def bench_module(path: str, steps: int, warmup: int, seed: int) -> dict:
+    """Time one saved module -- a rendered .hip (it carries its launch plan
+    and KERNEL_META) or a .json with a program key -- on seeded inputs,
+    the way reference bench.py:14-20,89-140 re-times any module exposing fn
+    and KERNEL_META: TFLOP/s from KERNEL_META's flops. Attention (Q, KT, V)
+    and MLP (X, W1, W2) modules are also checked against their closed form."""
+    import torch
+    from grammar.hip_module import HipModule
+    from grammar.workloads import torch_dtype
+    if path.endswith(".json"):
+        from grammar.kernel_ast import emit_module, program_from_key
+        with open(path) as f:
+            saved = json.load(f)
+        src = emit_module(program_from_key(saved["key"], saved.get("dtype")))
+    else:
+        with open(path) as f:
+            src = f.read()
+    mod = HipModule(src)
+    meta = mod.KERNEL_META
+    g = torch.Generator("cpu").manual_seed(seed)
+    dt = torch_dtype(mod.plan["dtype"])
+    named = {}
+    for name, shape in meta["inputs"]:
+        t = torch.randn(tuple(shape), generator=g)
+        if name in ("W1", "W2"):
+            t = t / math.sqrt(shape[0])
+        named[name] = t.to(dt).to("cuda")
+    tensors = dict(named)
+    tensors.update(mod.allocate("cuda"))
+    plan = mod.bind(tensors)
+    ms = timed(plan.run, steps, warmup)
+    out = tensors[mod.plan["outputs"][0]].float()
+    check = None
+    if set(named) == {"Q", "KT", "V"}:
+        import run_attention_search as RS
+        want = RS.attention_reference(1.0 / math.sqrt(named["Q"].shape[-1]))(named)
+    elif set(named) == {"X", "W1", "W2"}:
+        import run_mlp_search as MS
+        # build_mlp_ln's block ends in the normalised tensor "out", build_mlp_silu's in "y"
+        want = MS.mlp_reference("ln" if mod.plan["outputs"][0] == "out" else "silu")(named)
+    else:
+        want = None
+    if want is not None:
+        d = (out - want).abs()
+        tol = (1e-2, 1e-2) if mod.plan["dtype"] == "fp32" else (2e-2, 2e-3)
+        check = {"max_abs": float(d.max()), "mean_abs": float(d.mean()),
+                 "pass": float(d.max()) <= tol[0] and float(d.mean()) <= tol[1]}
+    flops = meta["flops"]
+    return {"metric": "module TFLOP/s (KERNEL_META flops)", "module": path, "value": round(flops / (ms * 1e-3) / 1e12, 3),
+            "unit": "TFLOP/s", "ms_per_step": round(ms, 6), "steps": steps, "warmup": warmup,
+            "clock_ramp_ms": CLOCK_RAMP_MS, "flops": flops, "flops_exact": meta.get("flops_exact"),
+            "dtype": mod.plan["dtype"], "stages": len(mod.plan["steps"]),
+            "lowering": [st["lowering"] for st in mod.plan["steps"]], "check": check}
 
 
 def best_so_far(timeline, flops: float) -> list:
@@ -352,12 +440,14 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=2000,
-                    help="untimed steps before the timed ones (at C2 about 50 ms: the GPU clocks ramp up "
-                         "over the first tens of milliseconds of load)")
+    ap.add_argument("--warmup", type=int, default=10,
+                    help="untimed steps before the timed ones; every leg then runs untimed steps for "
+                         f"{CLOCK_RAMP_MS:.0f} ms more while the GPU clocks ramp up (reported as clock_ramp_ms)")
     ap.add_argument("--config", default="C2", choices=["C2", "C3"])
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--kernel", default="descent", choices=["descent", "handwritten"])
+    ap.add_argument("--kernel", default="descent",
+                    help="descent | handwritten | PATH of a saved module (.hip as RunLogger writes it, or a "
+                         ".json holding a program key): re-time that module alone (reference bench.py --kernel)")
     ap.add_argument("--search-seconds", type=float, default=60.0, dest="search_seconds",
                     help="wall budget of the live descent (0 = use the committed best program)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -397,12 +487,16 @@ def main() -> int:
         log(f"[bench] copy calibration: {args.steps} copies of {args.copy_calibration} MiB")
         return 0
 
+    if args.kernel not in ("descent", "handwritten"):
+        print(json.dumps(bench_module(args.kernel, args.steps, args.warmup, args.seed)), flush=True)
+        return 0
+
     cfg = CONFIGS[args.config]
     peak = PEAK_TFLOPS[cfg.dtype]
-    if args.block_m is None:
-        args.block_m = 256 if cfg.D == 64 else 0
-    if args.block_n is None:
-        args.block_n = 128 if cfg.D == 64 else 0
+    from grammar.attention import default_tiles
+    dm, dn = default_tiles(cfg.N, cfg.D)
+    args.block_m = args.block_m or dm
+    args.block_n = args.block_n or dn
     q, k, v = (t.to(dev) for t in attention_inputs(cfg, seed=args.seed))
     kt = k.transpose(-1, -2).contiguous()
 
@@ -440,8 +534,9 @@ def main() -> int:
         kernel = {"name": "gr_flash_fwd (hand-written)", "block_m": args.block_m, "block_n": args.block_n}
         traffic_key = f"{cfg.name}:{cfg.dtype}:flash:bm{args.block_m}:bn{args.block_n}"
 
-    # 2. the timed region (exactly W warmup steps, then K timed ones)
-    ms = timed(step, args.steps, args.warmup, min_warm_s=0.0)
+    # 2. the timed region: W warmup steps, the clock ramp, then K timed steps
+    ms = timed(step, args.steps, args.warmup)
+    ramp_steps = _ramps[-1]
     tflops = cfg.flops / (ms * 1e-3) / 1e12
     log(f"[bench] {cfg.name} {kernel['name']}: {ms * 1e3:.2f} us/step  {tflops:.1f} TFLOP/s  "
         f"{100 * tflops / peak:.1f}% of peak")
@@ -495,12 +590,14 @@ def main() -> int:
         cpu["C1"] = c1
 
     rec = {
-        "metric": METRIC,
+        "metric": metric_for(cfg),
         "value": round(tflops, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_ramp_ms": CLOCK_RAMP_MS,
+        "clock_ramp_steps": ramp_steps,
         "ms_per_step": round(ms, 6),
         "higher_is_better": True,
         "scaling": "weak",

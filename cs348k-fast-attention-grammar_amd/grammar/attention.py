@@ -20,6 +20,15 @@ def _strides3(t, dims=(0, 1, 2)) -> "ctypes.Array":
     return rt._ll3(*(int(t.stride(d)) for d in dims))
 
 
+def default_tiles(N: int, D: int) -> tuple:
+    """(block_m, block_n) that gr_attn_fwd picks for block_m = block_n = 0:
+    the largest query tile of 256 / 128 / 64 dividing N, and 128 keys per
+    tile at D = 64 when they divide N, else 64 or 32."""
+    bm = 256 if N % 256 == 0 else 128 if N % 128 == 0 else 64
+    bn = 128 if (D == 64 and N % 128 == 0) else 64 if N % 64 == 0 else 32
+    return bm, bn
+
+
 def bind_flash_attention(q, k, v, *, causal: bool = False, scale: float | None = None,
                          k_transposed: bool = False, block_m: int = 0, block_n: int = 0,
                          out=None, stream=None):
