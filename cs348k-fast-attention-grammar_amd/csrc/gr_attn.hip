@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 
 #include "gr_flash_decode.h"
 #include "gr_host.h"
@@ -138,8 +139,18 @@ void decode_stream(const gr_attn_args& a, int S, hipStream_t st) {
 // per wave, up to 4 waves, 64-key tiles (32 when N is not a multiple of 64).
 // S > 1 splits the keys over S workgroups per head (or query tile) and merges
 // their partials through the workspace.
+// Message for a workspace smaller than the key split needs: the caller's
+// buffer (gr_attn_decode) or the library's fixed scratch array
+// (gr_attn_decode_noalloc).
+int workspace_short(bool fixed, size_t need, int S, size_t have) {
+  if (fixed)
+    return gr::fail(GR_E_ARG, "gr_attn_decode_noalloc: %d key parts need %zu bytes of scratch, more than the "
+                    "%zu-byte maximum (ask for fewer splits or use gr_attn_decode with a workspace)", S, need, have);
+  return gr::fail(GR_E_ARG, "gr_attn_decode: workspace of %zu bytes needed for %d key parts", need, S);
+}
+
 template <class T, int D>
-int launch_decode(gr_attn_args a, int S, void* ws, size_t ws_bytes, hipStream_t st) {
+int launch_decode(gr_attn_args a, int S, void* ws, size_t ws_bytes, bool fixed_ws, hipStream_t st) {
   if (a.Nq <= 4) {
     if (S < 1) S = 1;
     if (S > a.N / 32) S = a.N / 32;
@@ -148,8 +159,7 @@ int launch_decode(gr_attn_args a, int S, void* ws, size_t ws_bytes, hipStream_t 
     if ((long long)a.B * a.H > 0x7fffffffLL || S > 65535) return gr::fail(GR_E_ARG, "gr_attn_decode: grid out of range");
     if (S > 1) {
       const size_t need = gr_attn_decode_workspace(a.B, a.H, a.Nq, D, S);
-      if (!ws || ws_bytes < need)
-        return gr::fail(GR_E_ARG, "gr_attn_decode: workspace of %zu bytes needed for %d key parts", need, S);
+      if (!ws || ws_bytes < need) return workspace_short(fixed_ws, need, S, ws_bytes);
       a.part_o = static_cast<float*>(ws);
       a.part_ml = a.part_o + (size_t)S * a.B * a.H * a.Nq * D;
     }
@@ -177,8 +187,7 @@ int launch_decode(gr_attn_args a, int S, void* ws, size_t ws_bytes, hipStream_t 
   if (nblk > 0x7fffffffLL || S > 65535) return gr::fail(GR_E_ARG, "gr_attn_decode: grid out of range");
   if (S > 1) {
     const size_t need = gr_attn_decode_workspace(a.B, a.H, a.Nq, D, S);
-    if (!ws || ws_bytes < need)
-      return gr::fail(GR_E_ARG, "gr_attn_decode: workspace of %zu bytes needed for %d key parts", need, S);
+    if (!ws || ws_bytes < need) return workspace_short(fixed_ws, need, S, ws_bytes);
     a.part_o = static_cast<float*>(ws);
     a.part_ml = a.part_o + (size_t)S * a.B * a.H * a.Nq * D;
   }
@@ -285,21 +294,23 @@ extern "C" size_t gr_attn_decode_workspace(int B, int H, int Nq, int D, int spli
   return (size_t)splits * B * H * Nq * (D + 2) * sizeof(float);
 }
 
-extern "C" int gr_attn_decode(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H, int Nq,
-                              int N, int D, const long long* qs, const long long* ks, const long long* vs,
-                              const long long* os, float scale, int splits, void* workspace, size_t workspace_bytes,
-                              void* stream) {
-  if (!q || !k || !v || !o || !qs || !ks || !vs || !os) return gr::fail(GR_E_ARG, "gr_attn_decode: null argument");
-  if (B <= 0 || H <= 0 || Nq <= 0 || N <= 0) return gr::fail(GR_E_ARG, "gr_attn_decode: B, H, Nq, N must be positive");
-  if (N % 32 != 0) return gr::fail(GR_E_ARG, "gr_attn_decode: N=%d keys must be a multiple of 32", N);
+namespace {
+
+int attn_decode(const char* who, const void* q, const void* k, const void* v, void* o, int dtype, int B, int H,
+                int Nq, int N, int D, const long long* qs, const long long* ks, const long long* vs,
+                const long long* os, float scale, int splits, void* workspace, size_t workspace_bytes, bool fixed_ws,
+                void* stream) {
+  if (!q || !k || !v || !o || !qs || !ks || !vs || !os) return gr::fail(GR_E_ARG, "%s: null argument", who);
+  if (B <= 0 || H <= 0 || Nq <= 0 || N <= 0) return gr::fail(GR_E_ARG, "%s: B, H, Nq, N must be positive", who);
+  if (N % 32 != 0) return gr::fail(GR_E_ARG, "%s: N=%d keys must be a multiple of 32", who, N);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || ((uintptr_t)workspace & 15))
-    return gr::fail(GR_E_ARG, "gr_attn_decode: base pointers must be 16-byte aligned");
+    return gr::fail(GR_E_ARG, "%s: base pointers must be 16-byte aligned", who);
   const long long* all[4] = {qs, ks, vs, os};
   for (int t = 0; t < 4; ++t)
     for (int i = 0; i < 3; ++i)
       if (all[t][i] < 0 || (all[t][i] % 8) != 0)
-        return gr::fail(GR_E_ARG, "gr_attn_decode: strides must be non-negative multiples of 8 elements");
-  if (!(scale > 0.f)) return gr::fail(GR_E_ARG, "gr_attn_decode: scale must be positive");
+        return gr::fail(GR_E_ARG, "%s: strides must be non-negative multiples of 8 elements", who);
+  if (!(scale > 0.f)) return gr::fail(GR_E_ARG, "%s: scale must be positive", who);
   gr_attn_args a;
   a.q = q;
   a.k = k;
@@ -318,12 +329,62 @@ extern "C" int gr_attn_decode(const void* q, const void* k, const void* v, void*
   a.part_ml = nullptr;
   a.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = (hipStream_t)stream;
-#define GR_DT(TT)                                                                        \
-  if (D == 64) return launch_decode<TT, 64>(a, splits, workspace, workspace_bytes, st);  \
-  if (D == 128) return launch_decode<TT, 128>(a, splits, workspace, workspace_bytes, st); \
-  return gr::fail(GR_E_ARG, "gr_attn_decode: head dim D=%d unsupported (64 or 128)", D);
+#define GR_DT(TT)                                                                                  \
+  if (D == 64) return launch_decode<TT, 64>(a, splits, workspace, workspace_bytes, fixed_ws, st);  \
+  if (D == 128) return launch_decode<TT, 128>(a, splits, workspace, workspace_bytes, fixed_ws, st); \
+  return gr::fail(GR_E_ARG, "%s: head dim D=%d unsupported (64 or 128)", who, D);
   if (dtype == GR_F16) { GR_DT(_Float16) }
   if (dtype == GR_BF16) { GR_DT(__bf16) }
 #undef GR_DT
-  return gr::fail(GR_E_ARG, "gr_attn_decode: dtype %d unsupported (GR_F16 or GR_BF16)", dtype);
+  return gr::fail(GR_E_ARG, "%s: dtype %d unsupported (GR_F16 or GR_BF16)", who, dtype);
+}
+
+// The key-split partials of gr_attn_decode_noalloc live in this array, one
+// copy per device, held until the process ends. The kernels only ever see
+// its device address (g_scratch), which hipGetSymbolAddress returns for the
+// device current at the first call on it; the array's name is a host-side
+// stand-in and never goes to a kernel.
+constexpr size_t kDecodeScratch = (size_t)GR_DECODE_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kDecodeScratch];
+constexpr int kMaxDevices = 64;
+void* g_scratch[kMaxDevices] = {};
+std::mutex g_scratch_lock;
+
+int scratch_address(void** out) {
+  int dev = 0;
+  int rc = gr::hip_check(hipGetDevice(&dev), GR_E_RUNTIME, "gr_attn_decode_noalloc: hipGetDevice");
+  if (rc) return rc;
+  if (dev < 0 || dev >= kMaxDevices) return gr::fail(GR_E_ARG, "gr_attn_decode_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> hold(g_scratch_lock);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    rc = gr::hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), GR_E_RUNTIME,
+                       "gr_attn_decode_noalloc: hipGetSymbolAddress(scratch)");
+    if (rc) return rc;
+    if (!p) return gr::fail(GR_E_RUNTIME, "gr_attn_decode_noalloc: no device address for the scratch array");
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return GR_OK;
+}
+
+}  // namespace
+
+extern "C" int gr_attn_decode(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H, int Nq,
+                              int N, int D, const long long* qs, const long long* ks, const long long* vs,
+                              const long long* os, float scale, int splits, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  return attn_decode("gr_attn_decode", q, k, v, o, dtype, B, H, Nq, N, D, qs, ks, vs, os, scale, splits, workspace,
+                     workspace_bytes, false, stream);
+}
+
+extern "C" int gr_attn_decode_noalloc(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H,
+                                      int Nq, int N, int D, const long long* qs, const long long* ks,
+                                      const long long* vs, const long long* os, float scale, int splits,
+                                      void* stream) {
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc) return rc;
+  return attn_decode("gr_attn_decode_noalloc", q, k, v, o, dtype, B, H, Nq, N, D, qs, ks, vs, os, scale, splits, ws,
+                     kDecodeScratch, true, stream);
 }

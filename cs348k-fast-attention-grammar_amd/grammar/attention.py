@@ -268,6 +268,45 @@ def bind_flash_attention_decode(q, k, v, *, scale: float | None = None, splits: 
     return launch, out
 
 
+def bind_flash_attention_decode_noalloc(q, k, v, *, scale: float | None = None, splits: int = 0, out=None,
+                                        stream=None):
+    """(launch, out) for gr_attn_decode_noalloc: the decode launch with its
+    key-split partials in the library's per-device scratch array, so neither
+    the binding (given `out`) nor a launch allocates device memory. Launches
+    that overlap on one device race on that array. Raises if the split needs
+    more than rt.DECODE_SCRATCH_BYTES."""
+    import torch
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not t.is_cuda:
+            raise ValueError(f"flash_attention_decode_noalloc: {name} must be a GPU tensor (no CPU path)")
+        if t.dtype != q.dtype or t.dim() != 4 or t.stride(3) != 1:
+            raise ValueError(f"flash_attention_decode_noalloc: {name} must be 4-D, q's dtype, unit stride on D")
+    B, H, Nq, D = q.shape
+    N = k.shape[2]
+    if tuple(k.shape) != (B, H, N, D) or tuple(v.shape) != (B, H, N, D):
+        raise ValueError("flash_attention_decode_noalloc: k / v do not match q")
+    if out is None:
+        out = torch.empty((B, H, Nq, D), dtype=q.dtype, device=q.device)
+    elif tuple(out.shape) != (B, H, Nq, D) or out.dtype != q.dtype or out.stride(3) != 1:
+        raise ValueError("flash_attention_decode_noalloc: bad `out` tensor")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    L = rt.lib()
+    if splits <= 0:
+        splits = decode_splits(B, H, Nq, N, rt.device_info(q.device.index or 0)["cu_count"])
+    fn = L.gr_attn_decode_noalloc
+    args = (ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
+            ctypes.c_void_p(out.data_ptr()), rt.dtype_code(q.dtype), B, H, Nq, N, D,
+            _strides3(q), _strides3(k), _strides3(v), _strides3(out), float(scale), int(splits),
+            rt._stream_ptr(stream))
+    keep = (q, k, v, out)
+
+    def launch():
+        rt.check(fn(*args), "gr_attn_decode_noalloc")
+        return keep[3]
+    return launch, out
+
+
 def flash_attention_decode(q, k, v, *, scale: float | None = None, splits: int = 0, out=None,
                            workspace=None, stream=None):
     """O = softmax(scale * Q K^T) V for Nq queries against N keys (non-causal):

@@ -98,6 +98,8 @@ def lib() -> ctypes.CDLL:
         L.gr_attn_decode_workspace.restype = ctypes.c_size_t
         L.gr_attn_decode.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, _ll3, _ll3, _ll3, _ll3,
                                      ctypes.c_float, i32, vp, ctypes.c_size_t, vp]
+        L.gr_attn_decode_noalloc.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, _ll3, _ll3, _ll3, _ll3,
+                                             ctypes.c_float, i32, vp]
         _lib = L
         return L
 
@@ -108,8 +110,11 @@ EXPORTED = (
     "gr_module_load", "gr_module_free", "gr_get_kernel", "gr_launch", "gr_plan_create",
     "gr_plan_set_step", "gr_plan_run", "gr_plan_free", "gr_plan_time", "gr_attn_fwd",
     "gr_selftest_mfma32", "gr_gemm", "gr_mlp_fwd", "gr_attn_decode_workspace", "gr_attn_decode",
-    "gr_attn_fwd_train", "gr_attn_bwd_workspace", "gr_attn_bwd",
+    "gr_attn_fwd_train", "gr_attn_bwd_workspace", "gr_attn_bwd", "gr_attn_decode_noalloc",
 )
+
+# Bytes of the per-device scratch array behind gr_attn_decode_noalloc (GR_DECODE_SCRATCH_BYTES).
+DECODE_SCRATCH_BYTES = 16 << 20
 
 
 def last_error() -> str:

@@ -164,6 +164,24 @@ int gr_attn_decode(const void* q, const void* k, const void* v, void* o, int dty
                    const long long* v_strides, const long long* o_strides, float scale, int splits,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* gr_attn_decode without any allocation: no counterpart in the reference.
+ * For callers that cannot allocate device memory -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc. Same
+ * arguments and results as gr_attn_decode minus the workspace: the key-split
+ * partials go to a scratch array inside the library, GR_DECODE_SCRATCH_BYTES
+ * (16 MiB) per device, held by each device the library runs on until the
+ * process ends. A call whose key split needs more than that
+ * (gr_attn_decode_workspace(B, H, Nq, D, splits) after the split is clamped)
+ * fails with GR_E_ARG before launching anything. Nothing in the array needs
+ * to start at zero: every part overwrites its rows before the merge reads
+ * them. All calls on one device share its array, so calls that overlap in
+ * time on one device (different streams, threads) race: serialise them. */
+#define GR_DECODE_SCRATCH_BYTES (16u << 20)
+int gr_attn_decode_noalloc(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H, int Nq,
+                           int N, int D, const long long* q_strides, const long long* k_strides,
+                           const long long* v_strides, const long long* o_strides, float scale, int splits,
+                           void* stream);
+
 /* Batched GEMM with fused epilogue, C[z] = act(alpha * A[z] @ B[z]).
  * Replaces the grammar's matmul stage (a stage whose body is matmul over a
  * contraction axis, optionally followed by mulc and relu/silu:
