@@ -79,7 +79,16 @@ def _flt(x: float) -> str:
 # ---------------------------------------------------------------------------
 # Flash lowering
 # ---------------------------------------------------------------------------
-FLASH_BM = {32: (1, 1), 64: (2, 1), 128: (4, 1), 256: (8, 1)}   # block_m -> (waves, query blocks/wave)
+FLASH_BM = {32: (1, 1), 64: (2, 1), 128: (4, 1), 256: (8, 1)}   # block_m -> default (waves, query blocks/wave)
+
+# Schedule knobs of a flash-lowered stage (ParallelLoop.knobs), with their
+# choices: "qb" 32-query blocks per wave (the workgroup then has
+# block_m / (32 qb) waves; 2 halves the LDS fragment reads per MFMA at twice
+# the registers, head dim 64 only) and "pipe" the software-pipelined
+# schedule that issues the next key tile's score MFMAs during this tile's
+# softmax.
+FLASH_KNOBS = {"qb": (1, 2), "pipe": (0, 1)}
+FLASH_KNOB_DEFAULTS = {"qb": 1, "pipe": 0}     # what an absent knob means
 
 
 FLASH_DEFAULT_BN = {64: 128, 128: 64}    # key tile when the stage does not tile the key axis
@@ -208,11 +217,29 @@ def _match_flash(loop: ParallelLoop, program: Program):
     if N % BM or N % BN:
         return None
     nw, qb = FLASH_BM[BM]
+    knobs = getattr(loop, "knobs", {}) or {}
+    want_qb = int(knobs.get("qb", qb))
+    if want_qb in FLASH_KNOBS["qb"] and BM % (32 * want_qb) == 0 and not (D == 128 and want_qb > 1):
+        qb, nw = want_qb, BM // (32 * want_qb)        # a choice the tile cannot take keeps the default
+    pipe = 1 if int(knobs.get("pipe", 0)) else 0
     if D == 128 and qb > 1:
         return None
     return {"q": qload.source, "kt": ktload.source, "v": vload.source, "o": loop.out,
             "lead": _prod(qs[:nb]), "N": N, "D": D, "BM": BM, "BN": BN, "NW": nw, "QB": qb,
-            "causal": causal, "scale": scale}
+            "pipe": pipe, "causal": causal, "scale": scale}
+
+
+def schedule_knobs(loop: ParallelLoop, program: Program) -> dict:
+    """The schedule knobs the renderer honours for this stage, each with its
+    choices and current value: {name: (choices, current)}; empty for stages
+    that do not lower to the flash kernel."""
+    f = _match_flash(loop, program)
+    if f is None:
+        return {}
+    out = {"pipe": (FLASH_KNOBS["pipe"], f["pipe"])}
+    if f["D"] == 64:
+        out["qb"] = (FLASH_KNOBS["qb"], f["QB"])
+    return out
 
 
 def _render_flash(loop, program, f) -> tuple:
@@ -221,12 +248,13 @@ def _render_flash(loop, program, f) -> tuple:
     args = _loop_tensors(loop)
     params = ", ".join(f"{'const ' if a != loop.out else ''}{T}* __restrict__ {_cname(a)}" for a in args)
     N, D = f["N"], f["D"]
-    pipe = "false"
+    pipe = "true" if f.get("pipe") else "false"
     nt = f["NW"] * 64
     # K^T / V tiles straight into LDS when each thread moves whole 16-byte chunks
     direct = "true" if (D * f["BN"] // 8) % nt == 0 else "false"
     code = f"""
-// stage {loop.out}: flash attention (online softmax over key tiles of {f['BN']}, {f['BM']} queries/workgroup)
+// stage {loop.out}: flash attention (online softmax over key tiles of {f['BN']}, {f['BM']} queries/workgroup,
+// {f['NW']} waves of {f['QB']} x 32 queries{', software-pipelined' if f.get('pipe') else ''})
 extern "C" __global__ __launch_bounds__({nt})
 __attribute__((amdgpu_waves_per_eu(gr_flash_wpe<{D}, {f['BN']}, {f['NW']}, {f['QB']}, true, {pipe}>::value)))
 void {kname}({params}) {{
@@ -247,7 +275,8 @@ void {kname}({params}) {{
     lds = 2 * (f["BN"] * D * 2 + D * f["BN"] * 2)
     return code, {"kernel": kname, "grid": [grid, 1, 1], "block": [nt, 1, 1], "lds": lds,
                   "args": args, "lowering": "flash",
-                  "tiles": {"block_m": f["BM"], "block_n": f["BN"]}}
+                  "tiles": {"block_m": f["BM"], "block_n": f["BN"], "waves": f["NW"], "qb": f["QB"],
+                            "pipe": f.get("pipe", 0)}}
 
 
 # ---------------------------------------------------------------------------

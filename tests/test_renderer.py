@@ -77,13 +77,42 @@ def test_flash_lowering_selected_for_fp16_flash_structure():
     p = C.p_flash_attention(B=2, H=2, N=256, d=64, bm=128, bn=64, dtype="fp16")
     plan = parse_plan(emit_module(p))
     assert [s["lowering"] for s in plan["steps"]] == ["flash"]
-    assert plan["steps"][0]["tiles"] == {"block_m": 128, "block_n": 64}
+    assert plan["steps"][0]["tiles"] == {"block_m": 128, "block_n": 64, "waves": 4, "qb": 1, "pipe": 0}
     # same structure in fp32 has no 16-bit MFMA path: generic lowering
     p32 = C.p_flash_attention(B=2, H=2, N=256, d=64, bm=32, bn=32, dtype="fp32")
     assert parse_plan(emit_module(p32))["steps"][0]["lowering"] == "generic"
     # unsupported query tile -> generic (never a silent mismatch)
     p48 = C.p_flash_attention(B=1, H=1, N=256, d=64, bm=16, bn=64, dtype="fp16")
     assert parse_plan(emit_module(p48))["steps"][0]["lowering"] == "generic"
+
+
+def test_flash_schedule_knobs_reach_the_renderer_and_the_key():
+    """The flash stage's schedule knobs (query blocks per wave, software
+    pipelining) are descent parameters: they change the rendered kernel and
+    the structural key, survive program_from_key, and the renderer's default
+    is stored as an absent knob."""
+    from grammar import optimization as O
+    from grammar.kernel_ast import program_from_key, structural_key
+    p = C.p_flash_attention(B=2, H=2, N=512, d=64, bm=256, bn=64, dtype="fp16")
+    names = {q.name: q for q in O.parameter_vector(p)}
+    assert {"SCHED_O.qb", "SCHED_O.pipe"} <= set(names)
+    assert names["SCHED_O.qb"].ladder() == [1, 2] and names["SCHED_O.pipe"].current == 0
+    base_key, base_src = structural_key(p), emit_module(p)
+    names["SCHED_O.pipe"].set(1)
+    names["SCHED_O.qb"].set(2)
+    assert p.body[0].knobs == {"pipe": 1, "qb": 2}
+    tiles = parse_plan(emit_module(p))["steps"][0]["tiles"]
+    assert tiles == {"block_m": 256, "block_n": 64, "waves": 4, "qb": 2, "pipe": 1}
+    assert "gr_flash_fwd_body<_Float16, 64, 64, 4, 2, false, true, true," in emit_module(p)
+    key = structural_key(p)
+    assert key != base_key and structural_key(program_from_key(key)) == key
+    names["SCHED_O.pipe"].set(0)
+    names["SCHED_O.qb"].set(1)
+    assert p.body[0].knobs == {} and structural_key(p) == base_key and emit_module(p) == base_src
+    # head dim 128 offers no second query block per wave; non-flash stages offer nothing
+    p128 = C.p_flash_attention(B=1, H=2, N=256, d=128, bm=128, bn=64, dtype="bf16")
+    assert [q.name for q in O.parameter_vector(p128) if q.name.startswith("SCHED_")] == ["SCHED_O.pipe"]
+    assert not [q for q in O.parameter_vector(C.p_attention_atomic()) if q.name.startswith("SCHED_")]
 
 
 def test_lds_overflow_is_reported():

@@ -75,6 +75,12 @@ FLASH = [
     (1, 4, 512, 64, 256, 64, False, "bf16"),
     (1, 2, 256, 128, 128, 64, True, "bf16"),
     (1, 2, 256, 64, 32, 128, False, "fp16"),
+    # schedule knobs (descent parameters SCHED_O.pipe / SCHED_O.qb)
+    (1, 4, 512, 64, 256, 128, False, "fp16", {"pipe": 1}),
+    (1, 4, 512, 64, 256, 64, False, "fp16", {"qb": 2}),
+    (1, 4, 512, 64, 256, 64, True, "bf16", {"qb": 2, "pipe": 1}),
+    (1, 2, 256, 128, 128, 64, True, "bf16", {"pipe": 1}),
+    (2, 2, 256, 64, 128, 128, False, "bf16", {"qb": 2}),
 ]
 
 
@@ -83,10 +89,15 @@ def test_flash_lowered_program_parity(case):
     dev = _cuda()
     from grammar.hip_module import load_module
     from grammar.workloads import AttnConfig, attention_inputs
-    B, H, N, d, bm, bn, causal, dt = case
+    B, H, N, d, bm, bn, causal, dt = case[:8]
+    knobs = case[8] if len(case) > 8 else {}
     prog = C.p_flash_attention(B=B, H=H, N=N, d=d, bm=bm, bn=bn, causal=causal, dtype=dt)
+    prog.body[0].knobs.update(knobs)
+    print(f"[case] flash-lowered {case}", flush=True)
     mod = load_module(emit_module(prog))
     assert [s["lowering"] for s in mod.plan["steps"]] == ["flash"]
+    tiles = mod.plan["steps"][0]["tiles"]
+    assert tiles["qb"] == knobs.get("qb", 1) and tiles["pipe"] == knobs.get("pipe", 0)
     q, kt, v = attention_inputs(AttnConfig("t", B, H, N, d, dt, causal), seed=3, k_transposed=True)
     o = mod.fn(kt.to(dev), q.to(dev), v.to(dev))          # sorted input names: KT, Q, V
     torch.cuda.synchronize()
