@@ -240,6 +240,10 @@ int attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, i
       if (all[t][i] < 0 || (all[t][i] % 8) != 0)
         return gr::fail(GR_E_ARG, "gr_attn_fwd: strides must be non-negative multiples of 8 elements");
   if (!(scale > 0.f)) return gr::fail(GR_E_ARG, "gr_attn_fwd: scale must be positive");
+  // fp16 pre-scales Q by scale * log2(e) in fp16: above 1 a finite q could overflow
+  if (dtype == GR_F16 && scale * 1.4426950408889634f > 1.0f)
+    return gr::fail(GR_E_ARG, "gr_attn_fwd: fp16 needs scale * log2(e) <= 1 (scale <= 0.693; got %g); use bf16",
+                    (double)scale);
   gr_attn_args a;
   a.q = q;
   a.k = k;
@@ -311,6 +315,10 @@ int attn_decode(const char* who, const void* q, const void* k, const void* v, vo
       if (all[t][i] < 0 || (all[t][i] % 8) != 0)
         return gr::fail(GR_E_ARG, "%s: strides must be non-negative multiples of 8 elements", who);
   if (!(scale > 0.f)) return gr::fail(GR_E_ARG, "%s: scale must be positive", who);
+  // more than 4 queries run the flash body, which pre-scales Q in fp16 (see gr_attn_fwd)
+  if (dtype == GR_F16 && Nq > 4 && scale * 1.4426950408889634f > 1.0f)
+    return gr::fail(GR_E_ARG, "%s: fp16 with more than 4 queries needs scale * log2(e) <= 1 (got scale %g); use bf16",
+                    who, (double)scale);
   gr_attn_args a;
   a.q = q;
   a.k = k;

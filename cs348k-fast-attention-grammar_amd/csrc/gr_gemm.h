@@ -19,9 +19,10 @@
 //    gfx950's transposing LDS read (gr_tr_frag). 16-byte chunks are
 //    XOR-swizzled by row so the MFMA operand reads and the tile writes are
 //    conflict free.
-//  * Two LDS stages: the next k tile goes straight from global memory into
-//    one stage (global_load_lds, no staging registers) while the current one
-//    feeds the MFMAs; one barrier per k tile.
+//  * A ring of STAGES LDS stages: k tiles go straight from global memory into
+//    LDS (global_load_lds, no staging registers) STAGES - 1 tiles ahead of the
+//    one feeding the MFMAs; one barrier per k tile, and each wave waits only
+//    for the next tile's loads before it.
 //  * Tiles are walked in groups of GROUP_M tile rows (B columns reused from
 //    L2), and the group order is remapped so consecutive groups run on one XCD.
 //  * M and N need not be multiples of the tile (N a multiple of 8): edge
@@ -55,7 +56,15 @@ __device__ __forceinline__ float gr_epilogue(float v) {
   else return v;
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN>
+// s_waitcnt that waits only until at most N vector memory operations of this
+// wave are outstanding (expcnt and lgkmcnt left at their "no wait" maxima).
+template <int N>
+__device__ __forceinline__ void gr_wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int BM, int BN, int BK, int WGM, int WGN, int STAGES = 2>
 struct gr_gemm_cfg {
   static constexpr int NW = WGM * WGN;
   static constexpr int NT = NW * 64;
@@ -67,18 +76,19 @@ struct gr_gemm_cfg {
   static constexpr int B_BYTES = BN * BK * 2;
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr int C_BYTES = BM * BN * 2;     // the output tile, staged for coalesced stores
-  static constexpr int LDS = 2 * STAGE > C_BYTES ? 2 * STAGE : C_BYTES;
+  static constexpr int LDS = STAGES * STAGE > C_BYTES ? STAGES * STAGE : C_BYTES;
+  static_assert(STAGES >= 2, "at least a double-buffered ring");
   static_assert(WM % 32 == 0 && WN % 32 == 0, "each wave owns whole 32x32 blocks");
   static_assert(BK % 16 == 0 && BK >= 16, "k tile");
   // 16-byte operand reads use chunk pairs (2*ks + lane/32): a row needs >= 2 chunks
   static_assert(BK / 8 >= 2, "k tile");
 };
 
-template <class T, int BM, int BN, int BK, int WGM, int WGN, bool B_KMAJOR, int EPI>
+template <class T, int BM, int BN, int BK, int WGM, int WGN, bool B_KMAJOR, int EPI, int STAGES = 2>
 __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
   typedef gr_mfma<T> MF;
   typedef typename MF::vec8 vec8;
-  typedef gr_gemm_cfg<BM, BN, BK, WGM, WGN> G;
+  typedef gr_gemm_cfg<BM, BN, BK, WGM, WGN, STAGES> G;
   constexpr int NT = G::NT, TM = G::TM, TN = G::TN, CPR = BK / 8;
   constexpr int GROUP_M = 8;
 
@@ -116,7 +126,6 @@ __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
     for (int j = 0; j < TM; ++j) acc[i][j] = (gr_f32x16)(0.f);
 
   // one k tile of MFMAs from an LDS stage
-  // one k tile of MFMAs from an LDS stage
   auto frags = [&](const char* cur, int ks, vec8 (&bt)[TN], vec8 (&am)[TM]) {
 #pragma unroll
     for (int i = 0; i < TN; ++i) {
@@ -144,30 +153,56 @@ __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
     }
   };
 
-  // tiles go straight from global memory into the next LDS stage while the
-  // current one feeds the MFMAs; the stage is published after vmcnt drains
+  // Tiles go straight from global memory into a ring of STAGES LDS stages,
+  // STAGES - 1 k tiles ahead of the one feeding the MFMAs. Before the barrier
+  // that publishes tile kt + 1, each wave waits only for its own loads of that
+  // tile (the loads of the later tiles stay in flight; a wave's vector memory
+  // operations complete in order). The stage a load overwrites held tile
+  // kt - 1, whose last reads finished before the previous barrier.
   const int nk = a.K / BK;
   gr_lds_loader<T, BM, BK, NT> la;
   // A [K, N] B is copied into LDS as laid out in memory ([BK][BN], swizzled for
   // transposing reads) and its fragments are read back with gr_tr_frag; a
   // K-major B is already [BN][BK].
-  typename gr_cond<B_KMAJOR, gr_lds_loader<T, BN, BK, NT>, gr_lds_loader<T, BK, BN, NT, true>>::type lb;
+  typedef typename gr_cond<B_KMAJOR, gr_lds_loader<T, BN, BK, NT>, gr_lds_loader<T, BK, BN, NT, true>>::type LB;
+  LB lb;
   la.init(tid, a.a_sm, rows_ok);
   if constexpr (B_KMAJOR) lb.init(tid, a.b_s, cols_ok);
   else lb.init(tid, a.b_s, BK, cols_ok / 8);
-  la.load(A, lds);
-  lb.load(B, lds + G::A_BYTES);
-  __builtin_amdgcn_s_waitcnt(0);
+  // vector memory operations per thread and k tile (every thread issues the same count)
+  constexpr int PER_TILE = gr_lds_loader<T, BM, BK, NT>::PER + LB::PER;
+  // partial waits count loads: every thread must issue the same number per tile
+  static_assert(STAGES == 2 || ((BM * BK / 8) % NT == 0 && (BN * BK / 8) % NT == 0),
+                "a ring deeper than two stages needs whole 16-byte chunks per thread");
+  auto load_tile = [&](int kt) {
+    char* dst = lds + (kt % STAGES) * G::STAGE;
+    la.load(A + (long long)kt * BK, dst);
+    lb.load(B + (long long)kt * b_step, dst + G::A_BYTES);
+  };
+  // wait until tile `next` has landed, with `ahead` later tiles in flight
+  auto wait_for = [&](int ahead) {
+    if constexpr (STAGES >= 4) {
+      if (ahead >= 2) { gr_wait_vmcnt<2 * PER_TILE>(); return; }
+    }
+    if constexpr (STAGES >= 3) {
+      if (ahead >= 1) { gr_wait_vmcnt<PER_TILE>(); return; }
+    }
+    gr_wait_vmcnt<0>();
+  };
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < nk) load_tile(s);
+  {
+    const int issued = nk < STAGES - 1 ? nk : STAGES - 1;
+    wait_for(issued - 1);
+  }
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
-    const char* cur = lds + (kt & 1) * G::STAGE;
-    char* nxt = lds + ((kt + 1) & 1) * G::STAGE;
-    if (kt + 1 < nk) {
-      la.load(A + (long long)(kt + 1) * BK, nxt);
-      lb.load(B + (long long)(kt + 1) * b_step, nxt + G::A_BYTES);
-    }
-    mma_tile(cur);
-    __builtin_amdgcn_s_waitcnt(0);
+    if (kt + STAGES - 1 < nk) load_tile(kt + STAGES - 1);
+    mma_tile(lds + (kt % STAGES) * G::STAGE);
+    // tiles issued beyond kt + 1
+    const int last = kt + STAGES - 1 < nk ? kt + STAGES - 1 : nk - 1;
+    wait_for(last - (kt + 1) > 0 ? last - (kt + 1) : 0);
     __syncthreads();
   }
 
@@ -211,16 +246,16 @@ __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
 // loader offsets and addressing.
 template <int BM, int BN, int BK, int WGM, int WGN, bool B_KMAJOR>
 struct gr_gemm_wpe {
-  typedef gr_gemm_cfg<BM, BN, BK, WGM, WGN> G;
+  typedef gr_gemm_cfg<BM, BN, BK, WGM, WGN, 2> G;
   static constexpr int LOADER = (BM * BK / 8 + G::NT - 1) / G::NT + (BN * BK / 8 + G::NT - 1) / G::NT;
   static constexpr int EST = 16 * G::TN * G::TM + 4 * (G::TN + G::TM) + LOADER + 40;
   static constexpr int value = EST > 240 ? 1 : 2;
 };
 
-template <class T, int BM, int BN, int BK, int WGM, int WGN, bool B_KMAJOR, int EPI>
+template <class T, int BM, int BN, int BK, int WGM, int WGN, bool B_KMAJOR, int EPI, int STAGES = 2>
 __global__ __launch_bounds__(WGM * WGN * 64)
 __attribute__((amdgpu_waves_per_eu(gr_gemm_wpe<BM, BN, BK, WGM, WGN, B_KMAJOR>::value)))
 void gr_gemm_kernel(gr_gemm_args a) {
   extern __shared__ __attribute__((aligned(16))) char gr_lds[];
-  gr_gemm_body<T, BM, BN, BK, WGM, WGN, B_KMAJOR, EPI>(a, gr_lds);
+  gr_gemm_body<T, BM, BN, BK, WGM, WGN, B_KMAJOR, EPI, STAGES>(a, gr_lds);
 }

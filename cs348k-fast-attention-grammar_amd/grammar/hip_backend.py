@@ -1251,6 +1251,12 @@ def render_module(program: Program, fn_name: str = "fn") -> str:
     inputs, inter, outputs = _program_io(program)
     parts = ['#include "gr_gemm.h"', "",
              f"// generated from a grammar program: {len(program.body)} stage(s), storage {program.dtype}"]
+    # The fp16 flash kernel pre-scales Q by scale * log2(e) once and rounds it
+    # to fp16; with a factor above 1 a finite |q| could overflow, so such a
+    # module takes the kernel's per-score scaling instead (any scale is exact).
+    flash = [f for f in (_match_flash(l, program) for l in program.body) if f is not None]
+    if program.dtype == "fp16" and any(f["scale"] * LOG2E > 1.0 for f in flash):
+        parts.insert(0, "#define GR_FLASH_OPT 0  // a flash stage's scale * log2(e) exceeds 1: no fp16 Q pre-scale")
     steps = []
     over, excess = [], 0
     for loop in program.body:

@@ -103,8 +103,9 @@ int gr_plan_time(gr_plan* p, void* stream, int warmup, int iters, int mode, floa
  * reference point (flash-attn2-sota.py:41-62).
  *  dtype: GR_F16 or GR_BF16 (fp32 accumulate). With GR_F16 the kernel
  *  rounds Q * scale * log2(e) to fp16 once (the scores then need no per-score
- *  scaling), so |q| * scale * log2(e) must stay below 65504: always so when
- *  scale * log2(e) <= 1, as for the default 1/sqrt(D) with D >= 3.
+ *  scaling); that cannot overflow when scale * log2(e) <= 1 (as for the
+ *  default 1/sqrt(D) with D >= 3), and a larger fp16 scale is refused with
+ *  GR_E_ARG (bf16 takes any scale).
  *  Q, V, O: [B, H, N, D] with strides {batch, head, seq} in elements
  *  (unit stride along D). K: [B, H, N, D] if k_transposed == 0, else KT
  *  [B, H, D, N] whose k_strides = {batch, head, d} (unit stride along N).
@@ -150,6 +151,8 @@ int gr_attn_bwd(const void* q, const void* k, const void* v, const void* o, cons
  *  Q, O: [B, H, Nq, D]; K, V: [B, H, N, D]; strides {batch, head, seq} in
  *  elements (multiples of 8), unit stride along D. N a multiple of 32; D in
  *  {64, 128}; dtype GR_F16 or GR_BF16.
+ *  With GR_F16 and more than 4 queries, scale * log2(e) must be <= 1 (as for
+ *  gr_attn_fwd; GR_E_ARG otherwise).
  *  Up to 4 queries run on a streaming kernel (K and V read once straight
  *  into registers, scores on the VALU); more on the flash body's MFMA tiles.
  *  splits: workgroups per head (up to 4 queries) or per query tile that

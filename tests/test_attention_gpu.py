@@ -167,6 +167,9 @@ def test_rejects_bad_shapes():
     with pytest.raises(ValueError):
         from grammar.attention import flash_attention_fwd
         flash_attention_fwd(q.cpu(), q.cpu(), q.cpu())   # no CPU path
+    q = torch.zeros(1, 1, 256, 64, dtype=torch.float16, device=dev)
+    with pytest.raises(rt.GrError, match="log2"):
+        _run(q, q, q, scale=1.0)             # fp16 Q pre-scale would exceed 1: refused, not overflowed
 
 
 DECODE = [

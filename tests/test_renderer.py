@@ -115,6 +115,16 @@ def test_flash_schedule_knobs_reach_the_renderer_and_the_key():
     assert not [q for q in O.parameter_vector(C.p_attention_atomic()) if q.name.startswith("SCHED_")]
 
 
+def test_fp16_flash_with_large_scale_skips_the_q_prescale():
+    """The fp16 flash kernel rounds Q * scale * log2(e) to fp16; a module whose
+    flash stage has scale * log2(e) > 1 turns that off (GR_FLASH_OPT 0)."""
+    big = C.p_flash_attention(B=1, H=2, N=256, d=64, bm=128, bn=64, scale=1.0, dtype="fp16")
+    assert emit_module(big).startswith("#define GR_FLASH_OPT 0")
+    assert "GR_FLASH_OPT" not in emit_module(C.p_flash_attention(B=1, H=2, N=256, d=64, bm=128, bn=64, dtype="fp16"))
+    assert "GR_FLASH_OPT" not in emit_module(C.p_flash_attention(B=1, H=2, N=256, d=64, bm=128, bn=64, scale=1.0,
+                                                                 dtype="bf16"))
+
+
 def test_lds_overflow_is_reported():
     from grammar.kernel_ast import Program, ParallelLoop, Store
     # an fp32 matmul stage (generic lowering) whose operand tiles need 1.5 MiB

@@ -81,6 +81,8 @@ FLASH = [
     (1, 4, 512, 64, 256, 64, True, "bf16", {"qb": 2, "pipe": 1}),
     (1, 2, 256, 128, 128, 64, True, "bf16", {"pipe": 1}),
     (2, 2, 256, 64, 128, 128, False, "bf16", {"qb": 2}),
+    # scale 1 in fp16: no Q pre-scale (scale * log2(e) > 1)
+    (1, 2, 256, 64, 128, 64, True, "fp16", {}, 1.0),
 ]
 
 
@@ -91,7 +93,8 @@ def test_flash_lowered_program_parity(case):
     from grammar.workloads import AttnConfig, attention_inputs
     B, H, N, d, bm, bn, causal, dt = case[:8]
     knobs = case[8] if len(case) > 8 else {}
-    prog = C.p_flash_attention(B=B, H=H, N=N, d=d, bm=bm, bn=bn, causal=causal, dtype=dt)
+    scale = case[9] if len(case) > 9 else 1.0 / d ** 0.5
+    prog = C.p_flash_attention(B=B, H=H, N=N, d=d, bm=bm, bn=bn, causal=causal, scale=scale, dtype=dt)
     prog.body[0].knobs.update(knobs)
     print(f"[case] flash-lowered {case}", flush=True)
     mod = load_module(emit_module(prog))
@@ -101,7 +104,8 @@ def test_flash_lowered_program_parity(case):
     q, kt, v = attention_inputs(AttnConfig("t", B, H, N, d, dt, causal), seed=3, k_transposed=True)
     o = mod.fn(kt.to(dev), q.to(dev), v.to(dev))          # sorted input names: KT, Q, V
     torch.cuda.synchronize()
-    ref = O.attention(q.float().numpy(), kt.float().numpy(), v.float().numpy(), causal=causal, k_transposed=True)
+    ref = O.attention(q.float().numpy(), kt.float().numpy(), v.float().numpy(), causal=causal, k_transposed=True,
+                      scale=scale)
     mx, mn = O.errors(o.float().cpu().numpy(), ref)
     print(f"[flash-lowered] {case}: max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)
     assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL
