@@ -5,6 +5,7 @@
 #include <cstdint>
 
 #include "gr_gemm.h"
+#include "gr_gemm_f32.h"
 #include "gr_host.h"
 #include "grammar_rt.h"
 
@@ -57,6 +58,52 @@ int dispatch(const gr_gemm_args& a, int batch, bool km, int epi, int bm, int bn,
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// fp32 on the fp32 matrix cores (gr_gemm_f32.h): (block_m, block_n) in
+// {32, 64, 128}^2, one wave per 32 rows / columns up to 2 x 2 waves; k tile 32
+// when K allows, else 16 or 8. M and N must be multiples of the tile.
+template <int BM, int BN, bool KM, int EPI>
+int launch_gemm_f32(const gr_gemm_args& a, int batch, hipStream_t st) {
+  constexpr int WGM = BM >= 64 ? 2 : 1, WGN = BN >= 64 ? 2 : 1;
+  if (a.M % BM || a.N % BN)
+    return gr::fail(GR_E_ARG, "gr_gemm: fp32 needs M=%d, N=%d multiples of the tile %dx%d", a.M, a.N, BM, BN);
+  const long long nblk = (long long)(a.M / BM) * (a.N / BN);
+  if (nblk > 0x7fffffffLL || batch > 65535) return gr::fail(GR_E_ARG, "gr_gemm: grid out of range");
+#define GR_F32K(BK)                                                                                        \
+  hipLaunchKernelGGL((gr_gemm_f32_kernel<BM, BN, BK, WGM, WGN, KM, EPI>), dim3((unsigned)nblk, (unsigned)batch), \
+                     dim3(WGM * WGN * 64), (gr_gemm_f32_cfg<BM, BN, BK, WGM, WGN, KM>::LDS), st, a)
+  if (a.K % 32 == 0) GR_F32K(32);
+  else if (a.K % 16 == 0) GR_F32K(16);
+  else if (a.K % 8 == 0) GR_F32K(8);
+  else return gr::fail(GR_E_ARG, "gr_gemm: fp32 needs K=%d a multiple of 8", a.K);
+#undef GR_F32K
+  return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_gemm launch");
+}
+
+template <bool KM, int EPI>
+int dispatch_f32_tile(const gr_gemm_args& a, int batch, int bm, int bn, hipStream_t st) {
+  if (bm == 0) bm = a.M % 128 == 0 ? 128 : a.M % 64 == 0 ? 64 : 32;
+  if (bn == 0) bn = a.N % 128 == 0 ? 128 : a.N % 64 == 0 ? 64 : 32;
+#define GR_T(M_, N_) \
+  if (bm == M_ && bn == N_) return launch_gemm_f32<M_, N_, KM, EPI>(a, batch, st);
+  GR_T(32, 32) GR_T(32, 64) GR_T(32, 128) GR_T(64, 32) GR_T(64, 64) GR_T(64, 128)
+  GR_T(128, 32) GR_T(128, 64) GR_T(128, 128)
+#undef GR_T
+  return gr::fail(GR_E_ARG, "gr_gemm: unsupported fp32 tile (block_m=%d, block_n=%d)", bm, bn);
+}
+
+int dispatch_f32(const gr_gemm_args& a, int batch, bool km, int epi, int bm, int bn, hipStream_t st) {
+#define GR_CASE(K, E) \
+  if (km == K && epi == E) return dispatch_f32_tile<K, E>(a, batch, bm, bn, st);
+  GR_CASE(false, GR_EPI_NONE)
+  GR_CASE(false, GR_EPI_RELU)
+  GR_CASE(false, GR_EPI_SILU)
+  GR_CASE(true, GR_EPI_NONE)
+  GR_CASE(true, GR_EPI_RELU)
+  GR_CASE(true, GR_EPI_SILU)
+#undef GR_CASE
+  return gr::fail(GR_E_ARG, "gr_gemm: epilogue %d unsupported", epi);
+}
+
 }  // namespace
 
 extern "C" int gr_gemm(const void* a, const void* b, void* c, int dtype, int batch, int M, int N, int K,
@@ -64,15 +111,16 @@ extern "C" int gr_gemm(const void* a, const void* b, void* c, int dtype, int bat
                        int b_kmajor, int epilogue, float alpha, int block_m, int block_n, void* stream) {
   if (!a || !b || !c || !a_strides || !b_strides || !c_strides) return gr::fail(GR_E_ARG, "gr_gemm: null argument");
   if (batch <= 0 || M <= 0 || N <= 0 || K <= 0) return gr::fail(GR_E_ARG, "gr_gemm: sizes must be positive");
-  if (N % 8 != 0 || K % 32 != 0)
+  if (dtype != GR_F32 && (N % 8 != 0 || K % 32 != 0))
     return gr::fail(GR_E_ARG, "gr_gemm: N=%d must be a multiple of 8 and K=%d a multiple of 32", N, K);
   if (!aligned16(a) || !aligned16(b) || !aligned16(c))
     return gr::fail(GR_E_ARG, "gr_gemm: base pointers must be 16-byte aligned");
   const long long* all[3] = {a_strides, b_strides, c_strides};
+  const int sq = dtype == GR_F32 ? 4 : 8;    // elements per 16 bytes
   for (int t = 0; t < 3; ++t)
     for (int i = 0; i < 2; ++i)
-      if (all[t][i] < 0 || (all[t][i] % 8) != 0)
-        return gr::fail(GR_E_ARG, "gr_gemm: strides must be non-negative multiples of 8 elements");
+      if (all[t][i] < 0 || (all[t][i] % sq) != 0)
+        return gr::fail(GR_E_ARG, "gr_gemm: strides must be non-negative multiples of 16 bytes");
   // 32-bit per-thread offsets inside one tile walk: the rows a tile spans
   if (a_strides[1] > 0x3fffffffLL / 256 || b_strides[1] > 0x3fffffffLL / 256)
     return gr::fail(GR_E_ARG, "gr_gemm: row strides too large");
@@ -90,7 +138,8 @@ extern "C" int gr_gemm(const void* a, const void* b, void* c, int dtype, int bat
   hipStream_t st = (hipStream_t)stream;
   if (dtype == GR_F16) return dispatch<_Float16>(g, batch, b_kmajor != 0, epilogue, block_m, block_n, st);
   if (dtype == GR_BF16) return dispatch<__bf16>(g, batch, b_kmajor != 0, epilogue, block_m, block_n, st);
-  return gr::fail(GR_E_ARG, "gr_gemm: dtype %d unsupported (GR_F16 or GR_BF16)", dtype);
+  if (dtype == GR_F32) return dispatch_f32(g, batch, b_kmajor != 0, epilogue, block_m, block_n, st);
+  return gr::fail(GR_E_ARG, "gr_gemm: dtype %d unsupported (GR_F32, GR_F16 or GR_BF16)", dtype);
 }
 
 extern "C" int gr_mlp_fwd(const void* x, const void* w1, const void* w2, void* h, void* y, int dtype, int M,

@@ -1,8 +1,9 @@
 """Python face of the hand-written CDNA4 GEMM with fused epilogue (gr_gemm)
 and the two-GEMM MLP block (gr_mlp_fwd).
 
-`gemm(a, b)` computes act(alpha * a @ b) for fp16/bf16 GPU tensors, batched
-over leading dimensions -- the grammar's matmul stage with its mulc and
+`gemm(a, b)` computes act(alpha * a @ b) for fp16/bf16 GPU tensors (fp32
+accumulate) or fp32 ones (on the fp32 matrix cores; M and N multiples of 32),
+batched over leading dimensions -- the grammar's matmul stage with its mulc and
 relu/silu epilogue (grammar/kernel_ast.py:168-223). `mlp_fwd(x, w1, w2)` is
 Y = SiLU(X W1) W2, the MLP block of run_mlp_search.py:42-127 with silu as
 its activation.

@@ -293,6 +293,16 @@ def _gemm_lds(bm, bn, bk):
     return max(2 * (bm + bn) * bk * 2, bm * bn * 2)
 
 
+GEMM_F32_TILES = (32, 64, 128)
+
+
+def _gemm_f32_lds(bm, bn, bk, kmajor):
+    """LDS bytes of gr_gemm_f32_cfg: two stages of padded fp32 tiles."""
+    a = bm * (bk + 4)
+    b = bn * (bk + 4) if kmajor else bk * (bn + 8)
+    return 2 * 4 * (a + b)
+
+
 def _gemm_waves(bm, bn):
     wgm, wgn = GEMM_WAVES_M[bm], GEMM_WAVES_N[bn]
     if bm == 256 and bn == 256:
@@ -303,8 +313,10 @@ def _gemm_waves(bm, bn):
 def _match_gemm(loop: ParallelLoop, program: Program):
     """Return the GEMM parameters if `loop` computes act(alpha * A @ B) from two
     loaded operands (the matmul over its contraction axis, at full extent or
-    in one ReductionLoop, then mulc* and at most one relu/silu), else None."""
-    if program.dtype not in ("fp16", "bf16"):
+    in one ReductionLoop, then mulc* and at most one relu/silu), else None.
+    fp16/bf16 stages take gr_gemm.h, fp32 stages gr_gemm_f32.h (fp32 matrix
+    cores; tiles of 32, 64 or 128 dividing M and N)."""
+    if program.dtype not in ("fp16", "bf16", "fp32"):
         return None
     stores = [s for s in loop.body if isinstance(s, Store)]
     if len(stores) != 1 or stores[0].dest != loop.out:
@@ -384,6 +396,16 @@ def _match_gemm(loop: ParallelLoop, program: Program):
     if any(t != 1 for t in tile[:nb]):
         return None
     BM, BN = tile[nb], tile[nb + 1]
+    batch = _prod(out[:nb])
+    if program.dtype == "fp32":
+        if BM not in GEMM_F32_TILES or BN not in GEMM_F32_TILES or M % BM or N % BN or K % 8:
+            return None
+        BK = rl.tile if rl is not None and rl.tile in (8, 16, 32) and K % rl.tile == 0 else \
+            (32 if K % 32 == 0 else 16 if K % 16 == 0 else 8)
+        return {"a": aload.source, "b": bload.source, "c": loop.out, "M": M, "N": N, "K": K, "batch": batch,
+                "a_sb": M * K if a_batched else 0, "b_sb": K * N if b_batched else 0, "c_sb": M * N,
+                "kmajor": kmajor, "act": act, "alpha": alpha, "BM": BM, "BN": BN, "BK": BK,
+                "WGM": 2 if BM >= 64 else 1, "WGN": 2 if BN >= 64 else 1, "f32": True}
     if BM not in GEMM_WAVES_M or BN not in GEMM_WAVES_N:   # ragged M, N: edge tiles store their valid part
         return None
     BK = rl.tile if rl is not None else 64
@@ -396,7 +418,6 @@ def _match_gemm(loop: ParallelLoop, program: Program):
     if M * K % 8 or K * N % 8 or K % 8 or N % 8:
         return None
     wgm, wgn = _gemm_waves(BM, BN)
-    batch = _prod(out[:nb])
     return {"a": aload.source, "b": bload.source, "c": loop.out, "M": M, "N": N, "K": K, "batch": batch,
             "a_sb": M * K if a_batched else 0, "b_sb": K * N if b_batched else 0, "c_sb": M * N,
             "kmajor": kmajor, "act": act, "alpha": alpha, "BM": BM, "BN": BN, "BK": BK, "WGM": wgm, "WGN": wgn}
@@ -408,6 +429,27 @@ def _render_gemm(loop, program, f) -> tuple:
     args = _loop_tensors(loop)
     params = ", ".join(f"{'const ' if a != loop.out else ''}{T}* __restrict__ {_cname(a)}" for a in args)
     km = "true" if f["kmajor"] else "false"
+    if f.get("f32"):
+        nt = f["WGM"] * f["WGN"] * 64
+        code = f"""
+// stage {loop.out}: fp32 MFMA GEMM {f['M']}x{f['N']}x{f['K']} (x{f['batch']}), tile {f['BM']}x{f['BN']}x{f['BK']}
+extern "C" __global__ __launch_bounds__({nt})
+void {kname}({params}) {{
+  extern __shared__ __attribute__((aligned(16))) char gr_gemm_smem[];
+  gr_gemm_args a;
+  a.a = {_cname(f['a'])}; a.b = {_cname(f['b'])}; a.c = {_cname(f['c'])};
+  a.a_sb = {f['a_sb']}LL; a.a_sm = {f['K']};
+  a.b_sb = {f['b_sb']}LL; a.b_s = {f['K'] if f['kmajor'] else f['N']};
+  a.c_sb = {f['c_sb']}LL; a.c_sm = {f['N']};
+  a.M = {f['M']}; a.N = {f['N']}; a.K = {f['K']};
+  a.alpha = {_flt(f['alpha'])};
+  gr_gemm_f32_body<{f['BM']}, {f['BN']}, {f['BK']}, {f['WGM']}, {f['WGN']}, {km}, {f['act']}>(a, gr_gemm_smem);
+}}
+"""
+        grid = (f["M"] // f["BM"]) * (f["N"] // f["BN"])
+        return code, {"kernel": kname, "grid": [grid, f["batch"], 1], "block": [nt, 1, 1],
+                      "lds": _gemm_f32_lds(f["BM"], f["BN"], f["BK"], f["kmajor"]), "args": args,
+                      "lowering": "gemm", "tiles": {"block_m": f["BM"], "block_n": f["BN"], "block_k": f["BK"]}}
     tpl = f"{T}, {f['BM']}, {f['BN']}, {f['BK']}, {f['WGM']}, {f['WGN']}, {km}, {f['act']}"
     nt = f["WGM"] * f["WGN"] * 64
     code = f"""
@@ -1249,20 +1291,24 @@ def render_module(program: Program, fn_name: str = "fn") -> str:
     shapes = _infer_program(program)
     meta = kernel_meta(program, shapes)
     inputs, inter, outputs = _program_io(program)
-    parts = ['#include "gr_gemm.h"', "",
+    parts = ['#include "gr_gemm_f32.h"', "",
              f"// generated from a grammar program: {len(program.body)} stage(s), storage {program.dtype}"]
     # The fp16 flash kernel pre-scales Q by scale * log2(e) once and rounds it
     # to fp16; with a factor above 1 a finite |q| could overflow, so such a
     # module takes the kernel's per-score scaling instead (any scale is exact).
-    flash = [f for f in (_match_flash(l, program) for l in program.body) if f is not None]
+    flash = [f for f in (_match_flash(l, program) for l in program.body
+                         if (getattr(l, "knobs", None) or {}).get("lowering") != "generic") if f is not None]
     if program.dtype == "fp16" and any(f["scale"] * LOG2E > 1.0 for f in flash):
         parts.insert(0, "#define GR_FLASH_OPT 0  // a flash stage's scale * log2(e) exceeds 1: no fp16 Q pre-scale")
     steps = []
     over, excess = [], 0
     for loop in program.body:
-        f = _match_flash(loop, program)
-        gm = _match_gemm(loop, program) if f is None else None
-        rw = _match_rows(loop, program) if f is None and gm is None else None
+        # knobs {"lowering": "generic"} pins a stage to the generic LDS-tile
+        # lowering (diagnostics and tests of that lowering)
+        generic = (getattr(loop, "knobs", None) or {}).get("lowering") == "generic"
+        f = None if generic else _match_flash(loop, program)
+        gm = _match_gemm(loop, program) if f is None and not generic else None
+        rw = _match_rows(loop, program) if f is None and gm is None and not generic else None
         try:
             if f is not None:
                 code, step = _render_flash(loop, program, f)

@@ -190,12 +190,15 @@ int gr_attn_decode_noalloc(const void* q, const void* k, const void* v, void* o,
  * contraction axis, optionally followed by mulc and relu/silu:
  * grammar/kernel_ast.py:168-223 EMIT_RULES/CONST_OPS, :826-845 accumulator
  * and K loop) as rendered for the MLP (run_mlp_search.py:42-127).
- *  dtype: GR_F16 or GR_BF16 (fp32 accumulate); batch: number of matrices.
+ *  dtype: GR_F16 or GR_BF16 (fp32 accumulate), or GR_F32 (fp32 throughout, on
+ *  the fp32 matrix cores: tiles (block_m, block_n) in {32, 64, 128}^2, M and
+ *  N multiples of the tile, K a multiple of 8, strides multiples of 4);
+ *  batch: number of matrices.
  *  A: [batch][M][K], a_strides = {batch, row}; unit stride along K.
  *  B: [batch][K][N] (b_kmajor == 0, unit stride along N) or [batch][N][K]
  *     (b_kmajor != 0, unit stride along K); b_strides = {batch, row}.
  *  C: [batch][M][N], c_strides = {batch, row}; unit stride along N.
- *  Strides are in elements, multiples of 8; batch stride 0 broadcasts.
+ *  Strides are in elements, multiples of 8 (of 4 for GR_F32); batch stride 0 broadcasts.
  *  epilogue: GR_EPI_NONE, GR_EPI_RELU or GR_EPI_SILU, applied to alpha*acc.
  *  (block_m, block_n) in {(128,128), (256,128), (128,256), (256,256)}
  *  (0 = 256). Any M; N a multiple of 8; K a multiple of 32 (the square

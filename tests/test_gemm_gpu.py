@@ -80,6 +80,50 @@ def test_gemm_small_parity(case):
     _check(c, ref, f"gemm {case}")
 
 
+F32_CASES = [
+    # batch, M, N, K, epilogue, alpha, b_kmajor, tile: the fp32 matrix-core GEMM (gr_gemm_f32.h)
+    (1, 128, 128, 64, "none", 1.0, False, (64, 64)),
+    (1, 256, 512, 96, "silu", 0.5, False, (128, 128)),
+    (2, 64, 256, 136, "relu", 1.0, True, (32, 128)),
+    (1, 512, 64, 512, "none", 0.125, False, (128, 32)),
+    (3, 96, 32, 40, "none", 1.0, True, (32, 32)),
+    (1, 384, 256, 1024, "silu", 1.0, False, (0, 0)),
+]
+
+
+@pytest.mark.parametrize("case", F32_CASES, ids=lambda c: "-".join(map(str, c)))
+def test_gemm_fp32_parity(case):
+    """fp32 in, fp32 out, fp32 products and sums on v_mfma_f32_32x32x2_f32:
+    against float64 at 1e-4 relative to the output's scale."""
+    dev = _cuda()
+    from grammar.gemm import gemm
+    z, M, N, K, epi, alpha, km, (bm, bn) = case
+    print(f"[case] gemm fp32 z={z} M={M} N={N} K={K} {epi} alpha={alpha} kmajor={km} tile={bm}x{bn}", flush=True)
+    g = torch.Generator("cpu").manual_seed(13)
+    a = torch.randn((z, M, K), generator=g)
+    b = torch.randn((z, N, K) if km else (z, K, N), generator=g) / np.sqrt(K)
+    c = gemm(a.to(dev), b.to(dev), epilogue=epi, alpha=alpha, b_kmajor=km, block_m=bm, block_n=bn)
+    torch.cuda.synchronize()
+    b64 = b.double().numpy()
+    if km:
+        b64 = b64.transpose(0, 2, 1)
+    ref = _act(alpha * (a.double().numpy() @ b64), epi)
+    got = c.double().cpu().numpy()
+    err = np.abs(got - ref).max() / max(1.0, np.abs(ref).max())
+    print(f"[parity] gemm fp32 {case}: max rel {err:.2e}", flush=True)
+    assert c.dtype == torch.float32 and np.isfinite(got).all() and err <= 1e-4
+
+
+def test_gemm_fp32_rejects_ragged_tiles():
+    dev = _cuda()
+    from grammar import runtime as rt
+    from grammar.gemm import gemm
+    a = torch.zeros((100, 64), device=dev)
+    b = torch.zeros((64, 64), device=dev)
+    with pytest.raises(rt.GrError):
+        gemm(a, b, block_m=64, block_n=64)
+
+
 def test_gemm_broadcast_b_and_batch_views():
     """A [2,3,M,K] against one shared B [K,N] (batch stride 0), and a
     non-contiguous batch view of A (every other matrix)."""

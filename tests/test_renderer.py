@@ -34,8 +34,16 @@ def _loads(p):
     return [s for l in p.body for s in R.statements(l.body) if isinstance(s, Load)]
 
 
+def _generic(p):
+    """Pin every stage to the generic LDS-tile lowering (fp32 matmul stages
+    otherwise lower to the fp32 MFMA GEMM)."""
+    for l in p.body:
+        l.knobs["lowering"] = "generic"
+    return p
+
+
 def test_hoist_emits_subtile_reads_and_sink_removes_them():
-    p = C.p_matmul_reduction()
+    p = _generic(C.p_matmul_reduction())
     assert "GR_SUBTILE" not in emit_module(p)
     for src in ("x", "y"):
         p = R.hoist(p, [l for l in _loads(p) if l.source == src][0])
@@ -47,7 +55,7 @@ def test_hoist_emits_subtile_reads_and_sink_removes_them():
 
 
 def test_subtile_emits_accumulating_mma():
-    p = C.p_matmul_full_k()
+    p = _generic(C.p_matmul_full_k())
     mm = next(s for s in p.body[0].body if isinstance(s, Compute))
     src_full = emit_module(p)
     q = R.subtile_reduction(p, mm, "k", tile=32)
@@ -56,7 +64,7 @@ def test_subtile_emits_accumulating_mma():
 
 
 def test_unwrap_subtile_reproduces_source():
-    p = C.p_matmul_full_k()
+    p = _generic(C.p_matmul_full_k())
     mm = next(s for s in p.body[0].body if isinstance(s, Compute))
     w = R.subtile_reduction(p, mm, "k", tile=32)
     rl = next(s for s in w.body[0].body if isinstance(s, ReductionLoop))

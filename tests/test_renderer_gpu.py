@@ -51,7 +51,13 @@ def test_rendered_case_matches_interpreter(name):
 def test_rewrites_preserve_results_on_gpu():
     p = C.p_matmul_reduction()
     ins = C.inputs_for(p, 0)
-    base, _ = _gpu_run(p, ins)
+    gemm_out, mod = _gpu_run(p, ins)                  # fp32 matmul stage: the fp32 MFMA GEMM
+    assert [s["lowering"] for s in mod.plan["steps"]] == ["gemm"]
+    for l in p.body:                                  # the same program on the generic lowering
+        l.knobs["lowering"] = "generic"
+    base, mod = _gpu_run(p, ins)
+    assert [s["lowering"] for s in mod.plan["steps"]] == ["generic"]
+    assert np.allclose(gemm_out, base, rtol=1e-3, atol=1e-3)
     h = p
     for src in ("x", "y"):
         ld = [s for l in h.body for s in R.statements(l.body) if isinstance(s, Load) and s.source == src][0]
