@@ -416,13 +416,13 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
       ql.load(Qp + (long long)(qw + qb * 32 < Nq ? qw + qb * 32 : Nq - 1) * a.q_sn, q_stage(qb));
     }
   }
-  // CI (the straight schedule with transposing reads, GR_FLASH_OPT): Q is
-  // pre-scaled by c = scale log2(e) (rounded to T once: relative 2^-11 in fp16,
-  // 2^-8 in bf16) and the score MFMAs start from -base, so the scores come out
-  // as exponents of 2 relative to the base and p = 2^s needs no VALU multiply-
-  // add per score. m then holds the base in those units (scale log2(e) q.k).
-  // fp16 only: bf16 keeps Q as given.
-  constexpr bool CI = GR_FLASH_OPT && !PIPE && TR && gr_is_same<T, _Float16>::value;
+  // CI (transposing reads, GR_FLASH_OPT): Q is pre-scaled by c = scale
+  // log2(e) (rounded to T once: relative 2^-11 in fp16, 2^-8 in bf16) and the
+  // score MFMAs start from -base, so the scores come out as exponents of 2
+  // relative to the base and p = 2^s needs no VALU multiply-add per score. m
+  // then holds the base in those units (scale log2(e) q.k). fp16 only: bf16
+  // keeps Q as given.
+  constexpr bool CI = GR_FLASH_OPT && TR && gr_is_same<T, _Float16>::value;
   gr_f32x16 cinit[QB];
   auto prescale_q = [&]() {
     if constexpr (CI) {
@@ -513,8 +513,31 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
   // Two score buffers used in turn (the loop is unrolled by two), so handing
   // the next tile's scores over costs no register moves.
   gr_f32x16 sA[KB][QB], sB[PIPE ? KB : 1][QB];
+  // CI with PIPE: the base (in exponent units) each score buffer's MFMAs
+  // started from; slot j & 1 holds tile j's
+  float sbase[2][QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) sbase[0][qb] = sbase[1][qb] = 0.f;
   if (PIPE) {
     gr_flash_qk<T, D, BN, QB, KTR>(sA, ks0, qf, l32, g);
+    if constexpr (CI && !CAUSAL) {
+      // the first tile's max pass here, so that every tile takes the fast
+      // path: the base moves to the row max and the first scores follow it
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        float mt = -GR_INF;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sA[kb][qb][r]);
+        mt = fmaxf(mt, gr_xor32(mt));
+        m[qb] = mt;
+        sbase[0][qb] = mt;
+        cinit[qb] = (gr_f32x16)(-mt);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) sA[kb][qb] -= mt;
+      }
+    }
     __syncthreads();   // every wave is done with slot 0 of K before K_2 lands there
   }
 
@@ -586,25 +609,63 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
                 pt[kb][hf][qb] = gr_as<vec8>(pw);
               }
         };
-        gr_flash_qk_from<T, D, BN, QB, KTR>(s, ks0 + ODD * L::KS, qf, cinit, l32, g);
-        mask();
         bool fresh = false;
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) fresh |= m[qb] == -GR_INF;
         bool ok = false;
-        if (!gr_any(fresh)) {
+        if constexpr (PIPE) {
+          // This tile's scores were computed in the previous iteration from
+          // the base of that time (sbase). In one basic block, so that the
+          // scheduler can put the exponentials between the matrix ops: the
+          // next tile's score MFMAs from the current base, and P of this tile
+          // taken as if its base were still current. A tile whose base has
+          // moved since (a rescale in between), the first tile and a tile
+          // with an overflowed p take the slow path below.
+          mask();
+          bool stale = false;
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) {
+            stale |= sbase[ODD][qb] != -cinit[qb][0];
+            sbase[ODD ^ 1][qb] = -cinit[qb][0];
+          }
+          gr_flash_qk_from<T, D, BN, QB, KTR>(sn, ks0 + (ODD ^ 1) * L::KS, qf, cinit, l32, g);
           const float z[QB] = {};
           make_p(gr_ic<0>{}, z);
-          bool bad = false;
+          bool bad = fresh || stale;
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb) bad |= !(lt[qb] <= 3.0e38f);   // an inf (or NaN) p
           ok = !gr_any(bad);
+          // the next tile's K fragment reads first (their latency hides
+          // behind the first exponentials), then per 32-key half block of
+          // this tile its share of the score MFMAs and the exponentials,
+          // packing and sums of its 16 scores per query block
+          constexpr int NQK = KB * DS * QB;
+          constexpr int NRD = KB * DS * (KTR ? 2 : 1);
+          constexpr int GROUPS = KB * 2;
+          __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);              // K fragment reads (t+1)
+#pragma unroll
+          for (int i = 0; i < GROUPS; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, NQK / GROUPS, 0);   // score MFMAs (t+1)
+            __builtin_amdgcn_sched_group_barrier(0x002, 16 * QB, 0);        // softmax VALU (t)
+          }
+        } else {
+          gr_flash_qk_from<T, D, BN, QB, KTR>(s, ks0 + ODD * L::KS, qf, cinit, l32, g);
+          mask();
+          if (!gr_any(fresh)) {
+            const float z[QB] = {};
+            make_p(gr_ic<0>{}, z);
+            bool bad = false;
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) bad |= !(lt[qb] <= 3.0e38f);   // an inf (or NaN) p
+            ok = !gr_any(bad);
+          }
         }
         if (!ok) {
           float sh[QB];
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb) {
-            const float bt = (m[qb] == -GR_INF) ? 0.f : m[qb];   // the base these scores are relative to
+            // the base these scores are relative to
+            const float bt = PIPE ? sbase[ODD][qb] : ((m[qb] == -GR_INF) ? 0.f : m[qb]);
             float mt = -GR_INF;
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb)
@@ -784,7 +845,7 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
           }
         }
       }
-      if constexpr (PIPE) {
+      if constexpr (PIPE && !CI) {
         // Interleave: per 32-key half block, the next tile's K reads and score
         // MFMAs between this tile's exponentials and its P*V MFMAs, so the
         // matrix cores run while the VALU works on the softmax.

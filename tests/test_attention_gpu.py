@@ -266,7 +266,9 @@ def test_growing_row_max_takes_the_rebase_path(dt, causal, D):
     grow = s.amax(-1) - s[..., :64].amax(-1)
     assert float(grow.median()) > 16 * math.log(2), "inputs must force a rebase"
     ref = O.attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), causal=causal)
-    for bm, bn in ((128, 64), (256, 64)):
+    # 129 / 257: the pipelined schedule, whose next-tile scores were computed
+    # from the base before the move
+    for bm, bn in ((128, 64), (256, 64), (129, 64), (257, 64)):
         o = _run(q.to(dev), k.to(dev), v.to(dev), causal=causal, block_m=bm, block_n=bn)
         _check(o, ref, f"growing max {dt} causal={causal} D={D} {bm}x{bn}")
 
