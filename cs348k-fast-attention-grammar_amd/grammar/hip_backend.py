@@ -770,8 +770,9 @@ def _row_major(shape):
 
 
 class _StageGen:
-    def __init__(self, loop: ParallelLoop, program: Program, shapes: dict):
+    def __init__(self, loop: ParallelLoop, program: Program, shapes: dict, check: bool = False):
         self.loop, self.p, self.shapes = loop, program, shapes
+        self.check = check
         self.T = CTYPE[program.dtype]
         self.lines = []
         self.ind = 1
@@ -820,8 +821,23 @@ class _StageGen:
         self.nfl = max((o + sz for o, sz, _, _ in placed), default=0)
         return [f"  constexpr int {n} = {offs[n]};" for n in sorted(offs, key=lambda x: int(x[1:]))]
 
+    def sync_stmt(self) -> str:
+        return "GR_SYNC();" if self.check else "__syncthreads();"
+
     def sync(self):
-        self.emit("__syncthreads();")
+        self.emit(self.sync_stmt())
+
+    # LDS and global accesses: plain in the product build; in the checking
+    # build (gr_check.h) every LDS index is bounds- and race-checked and every
+    # global index bounds-checked
+    def lr(self, x) -> str:
+        return f"GR_LR({x})" if self.check else f"gr_lds[{x}]"
+
+    def lw(self, x) -> str:
+        return f"GR_LW({x})" if self.check else f"gr_lds[{x}]"
+
+    def gidx(self, i, n) -> str:
+        return f"GR_GI({i}, {n}LL)" if self.check else i
 
     def define(self, node, base, shape, axes, origin):
         if len(origin) != len(axes):
@@ -914,7 +930,7 @@ class _StageGen:
                 e = f"({c})*{t} + {ix}" if c != "0" else ix
                 terms.append(f"(long long)({e})*{gst[d]}" if gst[d] != 1 else f"(long long)({e})")
             gi = " + ".join(terms) if terms else "0"
-            self.emit(f"gr_lds[{base} + e] = (float){src}[{gi}];")
+            self.emit(f"{self.lw(f'{base} + e')} = (float){src}[{self.gidx(gi, _prod(g))}];")
         self.elem_loop(shp, body)
         self.sync()
         origin = [("0" if (c == "0" or g[d] == 1) else f"({c})*{shp[d]}") for d, c in enumerate(coords)]
@@ -941,7 +957,7 @@ class _StageGen:
                 if (c != "0" and tile[d] * _cdiv(g[d], tile[d]) != g[d]) or (c == "0" and v.shape[d] > g[d]):
                     conds.append(f"({e}) < {g[d]}")
             gi = " + ".join(terms) if terms else "0"
-            stmt = f"{dst}[{gi}] = ({self.T})gr_lds[{v.addr(idx)}];"
+            stmt = f"{dst}[{self.gidx(gi, _prod(g))}] = ({self.T}){self.lr(v.addr(idx))};"
             self.emit(f"if ({' && '.join(conds)}) {stmt}" if conds else stmt)
         self.elem_loop(v.shape, body)
         self.sync()
@@ -968,7 +984,7 @@ class _StageGen:
             base = self.alloc(out_shape)
 
             def body(idx):
-                a = [f"gr_lds[{v.addr(idx)}]" for v in ins]
+                a = [self.lr(v.addr(idx)) for v in ins]
                 if op == "causal":
                     p = axes.index(c.axis)
                     q = p - 1
@@ -978,7 +994,7 @@ class _StageGen:
                             f"? -GR_INF : {a[0]}")
                 else:
                     expr = _ew_expr(op, a, c.const)
-                self.emit(f"gr_lds[{base} + e] = {expr};")
+                self.emit(f"{self.lw(f'{base} + e')} = {expr};")
             self.elem_loop(out_shape, body)
             self.sync()
             self.define(c, base, out_shape, axes, wide.origin)
@@ -1028,8 +1044,8 @@ class _StageGen:
             ai = idx[:r - 2] + [idx[r - 2], "k"]
             bi = idx[:r - 2] + ["k", idx[r - 1]]
             self.emit("float s = 0.f;")
-            self.emit(f"for (int k = 0; k < {K}; ++k) s = fmaf(gr_lds[{a.addr(ai)}], gr_lds[{b.addr(bi)}], s);")
-            self.emit(f"gr_lds[{base} + e] {'+' if accumulate else ''}= s;")
+            self.emit(f"for (int k = 0; k < {K}; ++k) s = fmaf({self.lr(a.addr(ai))}, {self.lr(b.addr(bi))}, s);")
+            self.emit(f"{self.lw(f'{base} + e')} {'+' if accumulate else ''}= s;")
         self.elem_loop(out_shape, body)
 
     def emit_rowreduce(self, v, p, L, out_shape, base, op, acc_mode):
@@ -1040,13 +1056,13 @@ class _StageGen:
             ii = list(idx)
             ii[p] = "k"
             self.emit(f"float r = {init};")
-            self.emit(f"for (int k = 0; k < {L}; ++k) {{ const float x = gr_lds[{v.addr(ii)}]; r = {comb}; }}")
+            self.emit(f"for (int k = 0; k < {L}; ++k) {{ const float x = {self.lr(v.addr(ii))}; r = {comb}; }}")
             if acc_mode is None:
-                self.emit(f"gr_lds[{base} + e] = r;")
+                self.emit(f"{self.lw(f'{base} + e')} = r;")
             elif op == "rowmax":
-                self.emit(f"gr_lds[{base} + e] = fmaxf(gr_lds[{base} + e], r);")
+                self.emit(f"{self.lw(f'{base} + e')} = fmaxf({self.lr(f'{base} + e')}, r);")
             else:
-                self.emit(f"gr_lds[{base} + e] += r;")
+                self.emit(f"{self.lw(f'{base} + e')} += r;")
         self.elem_loop(out_shape, body)
 
     def emit_softmax_matmul_full(self, a, b, out_shape, base):
@@ -1058,12 +1074,12 @@ class _StageGen:
             ai = idx[:r - 2] + [idx[r - 2], "k"]
             bi = idx[:r - 2] + ["k", idx[r - 1]]
             self.emit("float m = -GR_INF;")
-            self.emit(f"for (int k = 0; k < {K}; ++k) m = fmaxf(m, gr_lds[{a.addr(ai)}]);")
+            self.emit(f"for (int k = 0; k < {K}; ++k) m = fmaxf(m, {self.lr(a.addr(ai))});")
             self.emit("if (m == -GR_INF) m = 0.f;")
             self.emit("float l = 0.f, s = 0.f;")
-            self.emit(f"for (int k = 0; k < {K}; ++k) {{ const float p = __expf(gr_lds[{a.addr(ai)}] - m); "
-                      f"l += p; s = fmaf(p, gr_lds[{b.addr(bi)}], s); }}")
-            self.emit(f"gr_lds[{base} + e] = s / l;")
+            self.emit(f"for (int k = 0; k < {K}; ++k) {{ const float p = __expf({self.lr(a.addr(ai))} - m); "
+                      f"l += p; s = fmaf(p, {self.lr(b.addr(bi))}, s); }}")
+            self.emit(f"{self.lw(f'{base} + e')} = s / l;")
         self.elem_loop(out_shape, body)
 
     # -- reduction loops -----------------------------------------------------
@@ -1125,13 +1141,13 @@ class _StageGen:
             pad = "  " * self.ind
             if a["op"] == "softmax_matmul":
                 R = _prod(a["shape"][:-1])
-                init.append(f"{pad}for (int e = threadIdx.x; e < {E}; e += {NT}) gr_lds[{a['base']} + e] = 0.f;")
-                init.append(f"{pad}for (int e = threadIdx.x; e < {R}; e += {NT}) {{ gr_lds[{a['m']} + e] = -GR_INF; "
-                            f"gr_lds[{a['l']} + e] = 0.f; }}")
+                init.append(f"{pad}for (int e = threadIdx.x; e < {E}; e += {NT}) {self.lw(a['base'] + ' + e')} = 0.f;")
+                init.append(f"{pad}for (int e = threadIdx.x; e < {R}; e += {NT}) {{ {self.lw(a['m'] + ' + e')} = -GR_INF; "
+                            f"{self.lw(a['l'] + ' + e')} = 0.f; }}")
             else:
                 v = "-GR_INF" if a["op"] == "rowmax" else "0.f"
-                init.append(f"{pad}for (int e = threadIdx.x; e < {E}; e += {NT}) gr_lds[{a['base']} + e] = {v};")
-        init.append("  " * self.ind + "__syncthreads();")
+                init.append(f"{pad}for (int e = threadIdx.x; e < {E}; e += {NT}) {self.lw(a['base'] + ' + e')} = {v};")
+        init.append("  " * self.ind + self.sync_stmt())
         self.lines[init_mark:init_mark] = init
         # finalise (online softmax -> o / l) and publish the values
         for p in rl.partials:
@@ -1139,7 +1155,8 @@ class _StageGen:
             if a["op"] == "softmax_matmul":
                 E = _prod(a["shape"])
                 N = a["shape"][-1]
-                self.emit(f"for (int e = threadIdx.x; e < {E}; e += {NT}) gr_lds[{a['base']} + e] /= gr_lds[{a['l']} + e / {N}];")
+                self.emit(f"for (int e = threadIdx.x; e < {E}; e += {NT}) "
+                          f"{self.lw(a['base'] + ' + e')} /= {self.lr(a['l'] + f' + e / {N}')};")
                 self.sync()
             self.define(p, a["base"], a["shape"], a["axes"], a["origin"])
         self.vals[id(rl)] = self.vals[id(rl.partials[0])]
@@ -1199,15 +1216,15 @@ class _StageGen:
         def rows(idx):
             si = idx[:r - 1] + ["k"]
             self.emit("float mt = -GR_INF;")
-            self.emit(f"for (int k = 0; k < {K}; ++k) mt = fmaxf(mt, gr_lds[{s.addr(si)}]);")
-            self.emit(f"const float mo = gr_lds[{a['m']} + e];")
+            self.emit(f"for (int k = 0; k < {K}; ++k) mt = fmaxf(mt, {self.lr(s.addr(si))});")
+            self.emit(f"const float mo = {self.lr(a['m'] + ' + e')};")
             self.emit("const float mn = fmaxf(mo, mt);")
             self.emit("const float ms = (mn == -GR_INF) ? 0.f : mn;")
             self.emit("const float al = __expf(mo - ms);")
             self.emit("float ls = 0.f;")
-            self.emit(f"for (int k = 0; k < {K}; ++k) ls += __expf(gr_lds[{s.addr(si)}] - ms);")
-            self.emit(f"gr_lds[{a['m']} + e] = mn; gr_lds[{a['alpha']} + e] = al;")
-            self.emit(f"gr_lds[{a['l']} + e] = gr_lds[{a['l']} + e] * al + ls;")
+            self.emit(f"for (int k = 0; k < {K}; ++k) ls += __expf({self.lr(s.addr(si))} - ms);")
+            self.emit(f"{self.lw(a['m'] + ' + e')} = mn; {self.lw(a['alpha'] + ' + e')} = al;")
+            self.emit(f"{self.lw(a['l'] + ' + e')} = {self.lr(a['l'] + ' + e')} * al + ls;")
         self.elem_loop(rshape, rows)
         self.sync()
 
@@ -1215,11 +1232,13 @@ class _StageGen:
             si = idx[:r - 1] + ["k"]
             vi = idx[:r - 2] + ["k", idx[r - 1]]
             self.emit(f"const int row = e / {N};")
-            self.emit(f"const float mn = gr_lds[{a['m']} + row];")
+            self.emit(f"const float mn = {self.lr(a['m'] + ' + row')};")
             self.emit("const float ms = (mn == -GR_INF) ? 0.f : mn;")
             self.emit("float acc = 0.f;")
-            self.emit(f"for (int k = 0; k < {K}; ++k) acc = fmaf(__expf(gr_lds[{s.addr(si)}] - ms), gr_lds[{v.addr(vi)}], acc);")
-            self.emit(f"gr_lds[{a['base']} + e] = gr_lds[{a['base']} + e] * gr_lds[{a['alpha']} + row] + acc;")
+            self.emit(f"for (int k = 0; k < {K}; ++k) acc = fmaf(__expf({self.lr(s.addr(si))} - ms), "
+                      f"{self.lr(v.addr(vi))}, acc);")
+            self.emit(f"{self.lw(a['base'] + ' + e')} = {self.lr(a['base'] + ' + e')} * "
+                      f"{self.lr(a['alpha'] + ' + row')} + acc;")
         self.elem_loop(shape, outs)
 
     # -- kernel ----------------------------------------------------------------
@@ -1244,16 +1263,30 @@ class _StageGen:
         consts = self.assign_lds()
         if self.nfl * 4 > LDS_LIMIT:
             raise LdsOverflow(loop.out, self.nfl * 4 - LDS_LIMIT)
+        # the checking build keeps two shadow words per LDS float behind the tiles
+        lds = self.nfl * 4 * (3 if self.check else 1)
+        if lds > LDS_LIMIT:
+            raise UnsupportedProgram(f"stage {loop.out}: the checking build needs {lds} B of LDS "
+                                     f"(three times the tiles' {self.nfl * 4} B); use smaller tiles")
         params = ", ".join(f"{'const ' if a != loop.out else ''}{self.T}* __restrict__ {_cname(a)}" for a in args)
+        if self.check:
+            params += ", unsigned int* __restrict__ gr_chk"
         code = [f"// stage {loop.out}: generic LDS-tile kernel, tile {tuple(loop.tile_shape)}, "
-                f"{self.nfl * 4} B LDS",
+                f"{self.nfl * 4} B LDS{' (checking build)' if self.check else ''}",
                 f'extern "C" __global__ __launch_bounds__({NT}) void {kname}({params}) {{',
                 f"  extern __shared__ __attribute__((aligned(16))) float gr_lds[];"]
         code += consts
+        if self.check:
+            code += [f"  constexpr int gr_nfl = {self.nfl};",
+                     "  unsigned int gr_epoch = 1u;",
+                     "  unsigned int* const gr_sh = reinterpret_cast<unsigned int*>(gr_lds + gr_nfl);",
+                     f"  for (int e = threadIdx.x; e < 2 * gr_nfl; e += {NT}) gr_sh[e] = 0u;",
+                     "  __syncthreads();"]
         code += self.lines
         code.append("}")
         return "\n".join(code) + "\n", {"kernel": kname, "grid": [_prod(grid), 1, 1], "block": [NT, 1, 1],
-                                          "lds": self.nfl * 4, "args": args, "lowering": "generic"}
+                                          "lds": lds, "args": args + (["__check__"] if self.check else []),
+                                          "lowering": "generic"}
 
 
 def _ew_expr(op, a, const):
@@ -1286,13 +1319,19 @@ def _ew_expr(op, a, const):
 PLAN_TAG = "GR_PLAN"
 
 
-def render_module(program: Program, fn_name: str = "fn") -> str:
+def render_module(program: Program, fn_name: str = "fn", check: bool = False) -> str:
+    """HIP source of the whole program (one kernel per stage) with its launch
+    plan in a trailing comment. check=True: the checking build, whose generic
+    stages count out-of-range LDS and global indices and LDS races between
+    barriers in a buffer bound as "__check__" (csrc/gr_check.h; the flash,
+    GEMM and row lowerings are the same as in the product build)."""
     validate(program)
     shapes = _infer_program(program)
     meta = kernel_meta(program, shapes)
     inputs, inter, outputs = _program_io(program)
-    parts = ['#include "gr_gemm_f32.h"', "",
-             f"// generated from a grammar program: {len(program.body)} stage(s), storage {program.dtype}"]
+    parts = ['#include "gr_gemm_f32.h"'] + (['#include "gr_check.h"'] if check else []) + [
+        "", f"// generated from a grammar program: {len(program.body)} stage(s), storage {program.dtype}"
+        + (" (checking build)" if check else "")]
     # The fp16 flash kernel pre-scales Q by scale * log2(e) once and rounds it
     # to fp16; with a factor above 1 a finite |q| could overflow, so such a
     # module takes the kernel's per-score scaling instead (any scale is exact).
@@ -1317,7 +1356,7 @@ def render_module(program: Program, fn_name: str = "fn") -> str:
             elif rw is not None:
                 code, step = _RowGen(loop, program, rw).render()
             else:
-                code, step = _StageGen(loop, program, shapes).render()
+                code, step = _StageGen(loop, program, shapes, check=check).render()
         except LdsOverflow as e:
             over.append(loop.out)
             excess += e.need
@@ -1328,6 +1367,8 @@ def render_module(program: Program, fn_name: str = "fn") -> str:
         raise LdsOverflow(",".join(over), excess)
     plan = {"fn": fn_name, "dtype": program.dtype, "inputs": inputs, "intermediates": inter, "outputs": outputs,
             "tensors": {k: list(v) for k, v in program.tensors.items()}, "steps": steps, "meta": meta}
+    if check:
+        plan["check"] = True
     parts.append(f"/*{PLAN_TAG} {json.dumps(plan, sort_keys=True)} {PLAN_TAG}*/")
     return "\n".join(parts) + "\n"
 

@@ -115,6 +115,13 @@ def compile_cached(src: str, name: str = "gr_module.hip") -> tuple:
 _TORCH_DT = {"fp32": "float32", "fp16": "float16", "bf16": "bfloat16"}
 
 
+# The checking build's findings buffer (csrc/gr_check.h): one count per kind,
+# then the first finding at words 8-10.
+CHECK_ARG = "__check__"
+CHECK_WORDS = 16
+CHECK_KINDS = ("lds_range", "global_range", "raw", "war", "waw")
+
+
 class HipModule:
     def __init__(self, src: str, code: bytes | None = None):
         self.src = src
@@ -132,20 +139,39 @@ class HipModule:
         return getattr(torch, _TORCH_DT[self.plan["dtype"]])
 
     def allocate(self, device="cuda") -> dict:
-        """NaN-filled intermediates and outputs."""
+        """NaN-filled intermediates and outputs (and, for a checking build,
+        the zeroed findings buffer "__check__")."""
         import torch
         out = {}
         for name in self.plan["intermediates"] + self.plan["outputs"]:
             out[name] = torch.full(tuple(self.plan["tensors"][name]), float("nan"), dtype=self.dtype, device=device)
+        if self.plan.get("check"):
+            out[CHECK_ARG] = torch.zeros(CHECK_WORDS, dtype=torch.int32, device=device)
         return out
+
+    @staticmethod
+    def check_report(tensors: dict) -> dict:
+        """The findings of a checking build's run (csrc/gr_check.h): counts per
+        kind and the first finding's kind, source line and index."""
+        w = [int(x) & 0xFFFFFFFF for x in tensors[CHECK_ARG].cpu().tolist()]
+        rep = {k: w[i] for i, k in enumerate(CHECK_KINDS)}
+        rep["first"] = CHECK_KINDS[w[8] - 1] if w[8] else None
+        rep["first_line"], rep["first_index"] = (w[9], w[10]) if w[8] else (None, None)
+        return rep
 
     def bind(self, tensors: dict) -> rt.Plan:
         """A launch plan with every stage's tensor arguments bound."""
+        import torch
         steps = []
         for st, k in zip(self.plan["steps"], self.kernels):
             args = []
             for a in st["args"]:
                 t = tensors[a]
+                if a == CHECK_ARG:
+                    if t.dtype != torch.int32 or t.numel() < CHECK_WORDS or not t.is_contiguous():
+                        raise ValueError(f"{CHECK_ARG}: need {CHECK_WORDS} contiguous int32")
+                    args.append(t.data_ptr())
+                    continue
                 if tuple(t.shape) != tuple(self.plan["tensors"][a]) or t.dtype != self.dtype or not t.is_contiguous():
                     raise ValueError(f"tensor {a}: need contiguous {self.plan['tensors'][a]} {self.dtype}, "
                                      f"got {tuple(t.shape)} {t.dtype}")

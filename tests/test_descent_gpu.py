@@ -151,3 +151,25 @@ def test_evaluator_rejects_a_variant_that_fails_the_checker(tmp_path, monkeypatc
     finally:
         good.close()
         bad.close()
+
+
+def test_evaluator_checking_build_gate(tmp_path, monkeypatch):
+    """checked_build: a variant with a generic stage also runs its checking
+    build (LDS/global bounds, LDS races between barriers) before it is timed;
+    the atomic attention program's stages report nothing and it is scored."""
+    _cuda()
+    monkeypatch.setenv("GR_CACHE_DIR", str(tmp_path / "co"))
+    import grammar_cases as C
+    from grammar.optimization import EvalConfig, Evaluator
+    from test_check_build import _generic, fit_for_check
+    prog = _generic(C.p_attention_atomic())
+    fit_for_check(prog)          # tiles whose shadow words fit in LDS
+    _case("evaluator: checking build of the atomic attention program")
+    ev = Evaluator(EvalConfig(seed=0, checked_build=True))
+    try:
+        loss = ev(prog)
+        st = ev.stats()
+        assert 0 < loss < 1e9, loss
+        assert st["checked_builds"] == 1 and st["check_findings"] == 0 and st["timed_variants"] == 1
+    finally:
+        ev.close()
