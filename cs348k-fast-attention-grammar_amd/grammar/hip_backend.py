@@ -93,6 +93,11 @@ FLASH_KNOB_DEFAULTS = {"qb": 1, "pipe": 0}     # what an absent knob means
 
 FLASH_DEFAULT_BN = {64: 128, 128: 64}    # key tile when the stage does not tile the key axis
 
+# fp32 flash stages (gr_flash_f32.h): each wave owns 32 queries and a chunk of
+# BN keys, and the stage's partials live in module-scope device arrays, capped
+# at this many bytes; the chunk defaults to N / 16 keys (at least 32)
+FLASH32_WS_LIMIT = 32 << 20
+
 
 def _flash_scores(x, scope_ids):
     """Walk the score operand of a softmax_matmul down to its Q K^T product.
@@ -143,7 +148,7 @@ def _match_flash(loop: ParallelLoop, program: Program):
     O = softmax_matmul(x, V) over the key axis j -- bare (full key range) or
     the sole partial of a ReductionLoop over j -- with x the scaled and
     optionally causally masked Q K^T of `_flash_scores`, and nothing else."""
-    if program.dtype not in ("fp16", "bf16"):
+    if program.dtype not in ("fp16", "bf16", "fp32"):
         return None
     stores = [s for s in loop.body if isinstance(s, Store)]
     if len(stores) != 1 or stores[0].dest != loop.out:
@@ -206,6 +211,8 @@ def _match_flash(loop: ParallelLoop, program: Program):
         return None
     if D not in (64, 128):
         return None
+    if program.dtype == "fp32":
+        return _match_flash32(loop, rl, tile, nb, N, D, causal, scale, qload, ktload, vload, _prod(qs[:nb]))
     BM = tile[nb]
     BN = rl.tile if rl is not None else FLASH_DEFAULT_BN[D]
     if tile[nb + 1] < D:
@@ -229,12 +236,31 @@ def _match_flash(loop: ParallelLoop, program: Program):
             "pipe": pipe, "causal": causal, "scale": scale}
 
 
+def _match_flash32(loop, rl, tile, nb, N, D, causal, scale, qload, ktload, vload, lead):
+    """fp32 flash stage parameters (gr_flash_f32.h): non-causal; block_m =
+    32 NW queries per workgroup (NW waves of 32), block_n = keys per wave (the
+    key reduction tile, else N / 16 but at least 32); the partials of all key
+    chunks must fit FLASH32_WS_LIMIT."""
+    if causal or tile[nb + 1] < D:
+        return None
+    BM = tile[nb]
+    BN = rl.tile if rl is not None else max(32, N // 16)
+    if BM not in FLASH_BM or BN % 32 or N % BN or N % BM:
+        return None
+    parts = N // BN
+    if parts * lead * N * (D + 2) * 4 > FLASH32_WS_LIMIT:
+        return None
+    return {"q": qload.source, "kt": ktload.source, "v": vload.source, "o": loop.out, "lead": lead,
+            "N": N, "D": D, "BM": BM, "BN": BN, "NW": BM // 32, "QB": 1, "pipe": 0, "causal": False,
+            "scale": scale, "f32": True, "parts": parts}
+
+
 def schedule_knobs(loop: ParallelLoop, program: Program) -> dict:
     """The schedule knobs the renderer honours for this stage, each with its
     choices and current value: {name: (choices, current)}; empty for stages
     that do not lower to the flash kernel."""
     f = _match_flash(loop, program)
-    if f is None:
+    if f is None or f.get("f32"):
         return {}
     out = {"pipe": (FLASH_KNOBS["pipe"], f["pipe"])}
     if f["D"] == 64:
@@ -242,7 +268,41 @@ def schedule_knobs(loop: ParallelLoop, program: Program) -> dict:
     return out
 
 
+def _render_flash32(loop, program, f) -> tuple:
+    kname = f"{_cname(loop.out)}_kernel"
+    args = _loop_tensors(loop)
+    params = ", ".join(f"{'const ' if a != loop.out else ''}float* __restrict__ {_cname(a)}" for a in args)
+    N, D, lead, parts, nw = f["N"], f["D"], f["lead"], f["parts"], f["NW"]
+    ws = _cname(loop.out)
+    code = f"""
+// stage {loop.out}: fp32 flash attention on the fp32 matrix cores ({f['BM']} queries/workgroup, {nw} waves of
+// 32 queries, {f['BN']} keys per wave, {parts} partial(s) per query merged by the last wave; the
+// workspace below is this module's, so two launches of it must not overlap)
+__device__ float gr_ws_{ws}[{parts * lead * N * D}];
+__device__ float gr_ml_{ws}[{parts * lead * N * 2}];
+__device__ unsigned int gr_cnt_{ws}[{lead * N // 32}];
+extern "C" __global__ __launch_bounds__({nw * 64})
+void {kname}({params}) {{
+  gr_attn_args a;
+  a.q = {_cname(f['q'])}; a.k = {_cname(f['kt'])}; a.v = {_cname(f['v'])}; a.o = {_cname(f['o'])};
+  a.q_sb = {N * D}LL; a.q_sh = 0; a.q_sn = {D};
+  a.k_sb = {N * D}LL; a.k_sh = 0; a.k_sn = {N};
+  a.v_sb = {N * D}LL; a.v_sh = 0; a.v_sn = {D};
+  a.o_sb = {N * D}LL; a.o_sh = 0; a.o_sn = {D};
+  a.B = {lead}; a.H = 1; a.N = {N}; a.Nq = {N};
+  a.scale_log2 = {_flt(f['scale'] * LOG2E)};
+  gr_flash32_fwd_body<{D}, {f['BN']}, {nw}, true>(a, gr_ws_{ws}, gr_ml_{ws}, gr_cnt_{ws});
+}}
+"""
+    grid = lead * parts * (N // f["BM"])
+    return code, {"kernel": kname, "grid": [grid, 1, 1], "block": [nw * 64, 1, 1], "lds": 0,
+                  "args": args, "lowering": "flash",
+                  "tiles": {"block_m": f["BM"], "block_n": f["BN"], "waves": nw, "parts": parts}}
+
+
 def _render_flash(loop, program, f) -> tuple:
+    if f.get("f32"):
+        return _render_flash32(loop, program, f)
     T = CTYPE[program.dtype]
     kname = f"{_cname(loop.out)}_kernel"
     args = _loop_tensors(loop)
@@ -1339,6 +1399,8 @@ def render_module(program: Program, fn_name: str = "fn", check: bool = False) ->
                          if (getattr(l, "knobs", None) or {}).get("lowering") != "generic") if f is not None]
     if program.dtype == "fp16" and any(f["scale"] * LOG2E > 1.0 for f in flash):
         parts.insert(0, "#define GR_FLASH_OPT 0  // a flash stage's scale * log2(e) exceeds 1: no fp16 Q pre-scale")
+    if any(f.get("f32") for f in flash):
+        parts.insert(parts.index('#include "gr_gemm_f32.h"') + 1, '#include "gr_flash_f32.h"')
     steps = []
     over, excess = [], 0
     for loop in program.body:

@@ -117,6 +117,50 @@ def test_flash_lowered_program_parity(case):
     assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL
 
 
+FLASH32 = [
+    # B, H, N, d, bm, bn: fp32 flash stage (gr_flash_f32.h), keys split over waves
+    (1, 1, 512, 64, 64, 32),       # the reference's own workload
+    (1, 1, 512, 64, 128, 512),     # one key chunk: the merge is the wave's own partial
+    (2, 3, 256, 64, 32, 64),
+    (1, 2, 256, 128, 256, 128),
+    (4, 1, 128, 64, 128, 32),
+]
+
+
+@pytest.mark.parametrize("case", FLASH32, ids=lambda c: "-".join(map(str, c)))
+def test_fp32_flash_stage_parity_and_relaunch(case):
+    """fp32 attention as one flash stage on the fp32 matrix cores: every
+    query block's partials are merged by the last wave of the block, whose
+    counter must be back at zero for the next launch -- three launches on the
+    same and on new inputs agree with the fp64 closed form at fp32 tolerance."""
+    dev = _cuda()
+    from grammar.hip_module import load_module
+    B, H, N, d, bm, bn = case
+    prog = C.p_flash_attention(B=B, H=H, N=N, d=d, bm=bm, bn=bn, dtype="fp32")
+    print(f"[case] fp32 flash {case}", flush=True)
+    mod = load_module(emit_module(prog))
+    assert [s["lowering"] for s in mod.plan["steps"]] == ["flash"]
+    assert mod.plan["steps"][0]["tiles"]["parts"] == N // bn
+    g = torch.Generator("cpu").manual_seed(5)
+    for rep in range(3):
+        q = torch.randn((B, H, N, d), generator=g)
+        kt = torch.randn((B, H, d, N), generator=g)
+        v = torch.randn((B, H, N, d), generator=g)
+        if rep == 2:
+            q, kt, v = prev
+        o = mod.fn(kt.to(dev), q.to(dev), v.to(dev))
+        torch.cuda.synchronize()
+        ref = O.attention(q.double().numpy(), kt.double().numpy(), v.double().numpy(), k_transposed=True,
+                          scale=1.0 / d ** 0.5)
+        err = float(np.max(np.abs(o.cpu().numpy() - ref)))
+        print(f"[flash32] {case} launch {rep}: max-abs {err:.2e}", flush=True)
+        assert err <= 1e-3
+        if rep == 0:
+            prev, first = (q, kt, v), o.clone()
+        if rep == 2:
+            assert torch.equal(o, first)      # the same inputs give the same bits on a later launch
+
+
 def test_generic_fp16_attention_matches_rounded_interpreter():
     dev = _cuda()
     from grammar.hip_module import load_module
