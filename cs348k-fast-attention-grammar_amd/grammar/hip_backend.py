@@ -237,21 +237,25 @@ def _match_flash(loop: ParallelLoop, program: Program):
 
 
 def _match_flash32(loop, rl, tile, nb, N, D, causal, scale, qload, ktload, vload, lead):
-    """fp32 flash stage parameters (gr_flash_f32.h): non-causal; block_m =
-    32 NW queries per workgroup (NW waves of 32), block_n = keys per wave (the
-    key reduction tile, else N / 16 but at least 32); the partials of all key
-    chunks must fit FLASH32_WS_LIMIT."""
+    """fp32 flash stage parameters (gr_flash_f32.h): non-causal. A workgroup
+    owns 32 queries and NW = block_m / 32 chunks of block_n keys (the key
+    reduction tile, else 32), one per wave; PARTS = N / (NW block_n)
+    workgroups per query block leave partials in module-scope device arrays
+    (capped at FLASH32_WS_LIMIT bytes) that the last of them merges."""
     if causal or tile[nb + 1] < D:
         return None
     BM = tile[nb]
-    BN = rl.tile if rl is not None else max(32, N // 16)
-    if BM not in FLASH_BM or BN % 32 or N % BN or N % BM:
+    BN = rl.tile if rl is not None else 32
+    if BM not in FLASH_BM or BN % 32:
         return None
-    parts = N // BN
-    if parts * lead * N * (D + 2) * 4 > FLASH32_WS_LIMIT:
+    nw = BM // 32
+    if (D // nw) % 16 or N % 32 or N % (nw * BN):
+        return None
+    parts = N // (nw * BN)
+    if parts > 1 and parts * lead * N * (D + 2) * 4 > FLASH32_WS_LIMIT:
         return None
     return {"q": qload.source, "kt": ktload.source, "v": vload.source, "o": loop.out, "lead": lead,
-            "N": N, "D": D, "BM": BM, "BN": BN, "NW": BM // 32, "QB": 1, "pipe": 0, "causal": False,
+            "N": N, "D": D, "BM": BM, "BN": BN, "NW": nw, "QB": 1, "pipe": 0, "causal": False,
             "scale": scale, "f32": True, "parts": parts}
 
 
@@ -274,15 +278,21 @@ def _render_flash32(loop, program, f) -> tuple:
     params = ", ".join(f"{'const ' if a != loop.out else ''}float* __restrict__ {_cname(a)}" for a in args)
     N, D, lead, parts, nw = f["N"], f["D"], f["lead"], f["parts"], f["NW"]
     ws = _cname(loop.out)
+    if parts > 1:
+        arrays = (f"// partials of the {parts} workgroups of each query block, merged by the last of them;\n"
+                  f"// they are this module's, so two launches of it must not overlap\n"
+                  f"__device__ float gr_ws_{ws}[{parts * lead * N * D}];\n"
+                  f"__device__ float gr_ml_{ws}[{parts * lead * N * 2}];\n"
+                  f"__device__ unsigned int gr_cnt_{ws}[{lead * N // 32}];\n")
+        ptrs = f"gr_ws_{ws}, gr_ml_{ws}, gr_cnt_{ws}"
+    else:
+        arrays, ptrs = "", "nullptr, nullptr, nullptr"
     code = f"""
-// stage {loop.out}: fp32 flash attention on the fp32 matrix cores ({f['BM']} queries/workgroup, {nw} waves of
-// 32 queries, {f['BN']} keys per wave, {parts} partial(s) per query merged by the last wave; the
-// workspace below is this module's, so two launches of it must not overlap)
-__device__ float gr_ws_{ws}[{parts * lead * N * D}];
-__device__ float gr_ml_{ws}[{parts * lead * N * 2}];
-__device__ unsigned int gr_cnt_{ws}[{lead * N // 32}];
-extern "C" __global__ __launch_bounds__({nw * 64})
+// stage {loop.out}: fp32 flash attention on the fp32 matrix cores (32 queries x {nw} chunk(s) of {f['BN']} keys
+// per workgroup, one chunk per wave, merged in LDS; {parts} workgroup(s) per query block)
+{arrays}extern "C" __global__ __launch_bounds__({nw * 64})
 void {kname}({params}) {{
+  extern __shared__ __attribute__((aligned(16))) char gr_flash_smem[];
   gr_attn_args a;
   a.q = {_cname(f['q'])}; a.k = {_cname(f['kt'])}; a.v = {_cname(f['v'])}; a.o = {_cname(f['o'])};
   a.q_sb = {N * D}LL; a.q_sh = 0; a.q_sn = {D};
@@ -291,11 +301,12 @@ void {kname}({params}) {{
   a.o_sb = {N * D}LL; a.o_sh = 0; a.o_sn = {D};
   a.B = {lead}; a.H = 1; a.N = {N}; a.Nq = {N};
   a.scale_log2 = {_flt(f['scale'] * LOG2E)};
-  gr_flash32_fwd_body<{D}, {f['BN']}, {nw}, true>(a, gr_ws_{ws}, gr_ml_{ws}, gr_cnt_{ws});
+  gr_flash32_fwd_body<{D}, {f['BN']}, {nw}, true, {parts}>(a, gr_flash_smem, {ptrs});
 }}
 """
-    grid = lead * parts * (N // f["BM"])
-    return code, {"kernel": kname, "grid": [grid, 1, 1], "block": [nw * 64, 1, 1], "lds": 0,
+    grid = lead * (N // 32) * parts
+    lds = (nw * 32 * (D + 4) + nw * 32 * 2) * 4 + 16          # gr_flash32_lds<D, NW>::BYTES
+    return code, {"kernel": kname, "grid": [grid, 1, 1], "block": [nw * 64, 1, 1], "lds": lds,
                   "args": args, "lowering": "flash",
                   "tiles": {"block_m": f["BM"], "block_n": f["BN"], "waves": nw, "parts": parts}}
 

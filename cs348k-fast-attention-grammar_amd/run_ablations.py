@@ -11,7 +11,7 @@ The default workload is the reference's own: one head, N = 512, d = 64, fp32,
 64 iterations, Stage 2 every 4 iterations with K = 5, seed 0 -- the runs
 behind results/attn-*.json. --b/--h/--n/--d/--dtype select another one.
 
-    python run_ablations.py --out runs/ablations/ref_n512_fp32 [--budget 120]
+    python run_ablations.py --out runs/ablations/ref_n512_fp32 [--budget 120] [--rules reference]
 
 Each run directory gets config.json, log.jsonl, kernels/best_it*.{hip,json}
 (RunLogger), results/it*.json (the re-timed best kernels) and summary.json.
@@ -119,6 +119,8 @@ def main(argv=None) -> int:
     ap.add_argument("--budget", type=float, default=0.0, help="wall seconds per descent (0 = all iterations)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--retime-steps", type=int, default=200, dest="retime_steps")
+    ap.add_argument("--rules", default="full", choices=["full", "reference"],
+                    help="this grammar's rule set or the reference's seven rules")
     args = ap.parse_args(argv)
 
     import run_attention_search as RS
@@ -127,7 +129,7 @@ def main(argv=None) -> int:
         run_dir = os.path.join(args.out, principle)
         cli = ["--n", str(args.n), "--d", str(args.d), "--dtype", args.dtype, "--iters", str(args.iters),
                "--every", "4", "--k", "5", "--seed", str(args.seed), "--principle", principle,
-               "--run-dir", run_dir, "--time-budget", str(args.budget)]
+               "--run-dir", run_dir, "--time-budget", str(args.budget), "--rules", args.rules]
         if args.b is not None:
             cli += ["--b", str(args.b)]
         if args.h is not None:
@@ -151,7 +153,7 @@ def main(argv=None) -> int:
         print(f"===== {principle}: {summary[principle]['best_kind']} best {summary[principle]['best_loss_ms']} ms, "
               f"{len(retimed)} best kernels re-timed", flush=True)
     with open(os.path.join(args.out, "summary.json"), "w") as f:
-        json.dump({"workload": {k: getattr(args, k) for k in ("b", "h", "n", "d", "dtype", "iters", "seed")},
+        json.dump({"workload": {k: getattr(args, k) for k in ("b", "h", "n", "d", "dtype", "iters", "seed", "rules")},
                    "principles": summary}, f, indent=1)
     return 0
 

@@ -48,3 +48,15 @@ def test_run_ablations_covers_every_principle():
     for p in A.PRINCIPLES:
         cfg = RS.principle_config(p)
         assert set(cfg) >= {"rules", "repairable", "couple_tiles", "reduction_tile"}
+
+
+def test_reference_rule_set_ablations():
+    """--rules reference: the reference's seven rules, and without the inverse
+    rules for no_reversibility (reference run_attention_search.py:140-166)."""
+    import run_attention_search as RS
+    from grammar.optimization import REFERENCE_RULES
+    assert RS.principle_config("full", "reference")["rules"] == REFERENCE_RULES
+    norev = RS.principle_config("no_reversibility", "reference")["rules"]
+    assert "hoist" not in norev and "unwrap_reduction" not in norev and set(norev) < set(REFERENCE_RULES)
+    assert RS.principle_config("no_repairability", "reference")["repairable"] is False
+    assert "fuse_softmax_chain" in RS.principle_config("full")["rules"]

@@ -118,12 +118,14 @@ def test_flash_lowered_program_parity(case):
 
 
 FLASH32 = [
-    # B, H, N, d, bm, bn: fp32 flash stage (gr_flash_f32.h), keys split over waves
-    (1, 1, 512, 64, 64, 32),       # the reference's own workload
-    (1, 1, 512, 64, 128, 512),     # one key chunk: the merge is the wave's own partial
-    (2, 3, 256, 64, 32, 64),
-    (1, 2, 256, 128, 256, 128),
-    (4, 1, 128, 64, 128, 32),
+    # B, H, N, d, bm, bn: fp32 flash stage (gr_flash_f32.h): bm / 32 waves per
+    # workgroup, bn keys per wave, N / (bm / 32 * bn) workgroups per query block
+    (1, 1, 512, 64, 128, 32),      # the reference's own workload: 4 parts
+    (1, 1, 512, 64, 128, 128),     # one workgroup per query block: no workspace
+    (1, 1, 512, 64, 32, 32),       # 16 parts of one wave each
+    (2, 3, 256, 64, 64, 64),
+    (1, 2, 256, 128, 256, 32),     # 8 waves, d = 128
+    (4, 1, 128, 64, 32, 128),
 ]
 
 
@@ -140,7 +142,7 @@ def test_fp32_flash_stage_parity_and_relaunch(case):
     print(f"[case] fp32 flash {case}", flush=True)
     mod = load_module(emit_module(prog))
     assert [s["lowering"] for s in mod.plan["steps"]] == ["flash"]
-    assert mod.plan["steps"][0]["tiles"]["parts"] == N // bn
+    assert mod.plan["steps"][0]["tiles"]["parts"] == N // (bm // 32 * bn)
     g = torch.Generator("cpu").manual_seed(5)
     for rep in range(3):
         q = torch.randn((B, H, N, d), generator=g)
