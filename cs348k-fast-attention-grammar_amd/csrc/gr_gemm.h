@@ -1,12 +1,12 @@
 // gr_gemm.h -- batched MFMA GEMM with a fused elementwise epilogue, gfx950.
 //
-//   C[z] = act(alpha * A[z] @ B[z])      A [M, K] (unit stride on K)
-//                                        B [K, N] (unit stride on N), or K-major [N, K]
-//                                        C [M, N] (unit stride on N), fp32 accumulate
+//   C[z] = act(alpha * A[z] @ B[z]) [+ R[z]]   A [M, K] (unit stride on K)
+//                                              B [K, N] (unit stride on N), or K-major [N, K]
+//                                              C, R [M, N] (unit stride on N), fp32 accumulate
 //
 // This is the grammar's matmul stage (Compute("matmul") over a contraction
-// axis, optionally followed by mulc and relu/silu) and the two GEMMs of the
-// MLP block (silu after the first).
+// axis, optionally followed by mulc, relu/silu and the add of a loaded
+// residual tensor) and the two GEMMs of the MLP block (silu after the first).
 //
 // Design (one workgroup = WGM x WGN waves = a BM x BN tile of C):
 //  * The contraction runs on v_mfma_f32_32x32x16 in the transposed form
@@ -35,6 +35,7 @@
 #define GR_EPI_NONE 0
 #define GR_EPI_RELU 1
 #define GR_EPI_SILU 2
+#define GR_EPI_RES 4     // flag: + R after the activation (residual add, in fp32 before the rounding)
 #endif
 
 struct gr_gemm_args {
@@ -46,12 +47,14 @@ struct gr_gemm_args {
   long long c_sb, c_sm;   // batch stride, row stride of C
   int M, N, K;
   float alpha;
+  const void* r = nullptr;        // residual R (GR_EPI_RES), laid out like C
+  long long r_sb = 0, r_sm = 0;   // its batch and row strides
 };
 
 template <int EPI>
 __device__ __forceinline__ float gr_epilogue(float v) {
-  if constexpr (EPI == GR_EPI_RELU) return v > 0.f ? v : 0.f;
-  else if constexpr (EPI == GR_EPI_SILU)
+  if constexpr ((EPI & 3) == GR_EPI_RELU) return v > 0.f ? v : 0.f;
+  else if constexpr ((EPI & 3) == GR_EPI_SILU)
     return v * __builtin_amdgcn_rcpf(1.f + gr_exp2(v * -1.4426950408889634f));
   else return v;
 }
@@ -212,6 +215,9 @@ __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
   // tiles) so that the global stores are whole 16-byte chunks of contiguous
   // row segments. The main loop's final barrier has retired every operand read.
   constexpr int OCPR = BN / 8;
+  const T* R = (EPI & GR_EPI_RES)
+                   ? static_cast<const T*>(a.r) + z * a.r_sb + (long long)tm * BM * a.r_sm + (long long)tn * BN
+                   : nullptr;
 #pragma unroll
   for (int j = 0; j < TM; ++j) {
     const int row = wm * G::WM + j * 32 + l32;
@@ -219,13 +225,26 @@ __device__ __forceinline__ void gr_gemm_body(const gr_gemm_args& a, char* lds) {
     for (int i = 0; i < TN; ++i)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int chunk = (wn * G::WN + i * 32 + 8 * q) >> 3;
+        const int col = wn * G::WN + i * 32 + 8 * q + 4 * g;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + e]);
+        if constexpr ((EPI & GR_EPI_RES) != 0) {
+          // the residual's 4 values of this lane (rows and columns past the
+          // edge of C are never stored, and not read)
+          if (row < rows_ok && col < cols_ok) {
+            const gr_u32x2 rw = *reinterpret_cast<const gr_u32x2*>(R + (long long)row * a.r_sm + col);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const unsigned short h = (unsigned short)(rw[e >> 1] >> (16 * (e & 1)));
+              v[e] += (float)__builtin_bit_cast(T, h);
+            }
+          }
+        }
         gr_u32x2 w;
-        w[0] = gr_pack2f<T>(gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + 0]),
-                            gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + 1]));
-        w[1] = gr_pack2f<T>(gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + 2]),
-                            gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + 3]));
-        *reinterpret_cast<gr_u32x2*>(lds + row * (BN * 2) + gr_swz<OCPR>(row, chunk) * 16 + g * 8) = w;
+        w[0] = gr_pack2f<T>(v[0], v[1]);
+        w[1] = gr_pack2f<T>(v[2], v[3]);
+        *reinterpret_cast<gr_u32x2*>(lds + row * (BN * 2) + gr_swz<OCPR>(row, col >> 3) * 16 + g * 8) = w;
       }
   }
   __syncthreads();

@@ -1,7 +1,8 @@
 // gr_gemm_f32.h -- batched fp32 GEMM with a fused epilogue on the fp32 matrix
 // cores of gfx950 (v_mfma_f32_32x32x2_f32), for the grammar's fp32 programs.
 //
-//   C[z] = act(alpha * A[z] @ B[z])   A [M, K], B [K, N] or K-major [N, K], C [M, N]
+//   C[z] = act(alpha * A[z] @ B[z]) [+ R[z]]   A [M, K], B [K, N] or K-major [N, K],
+//                                              C, R [M, N]
 //
 // The reference's programs are fp32 end to end; without this their matmul
 // stages would run on the generic LDS lowering's scalar FMAs.
@@ -151,17 +152,23 @@ __device__ __forceinline__ void gr_gemm_f32_body(const gr_gemm_args& a, char* ld
 
   // lane (l32, g) of block (i, j): row m = wm*WM + 32j + l32, columns
   // n = wn*WN + 32i + 8q + 4g + (0..3) in accumulators 4q..4q+3
+  const float* R = (EPI & GR_EPI_RES) ? static_cast<const float*>(a.r) + z * a.r_sb +
+                                            (long long)tm * BM * a.r_sm + (long long)tn * BN
+                                      : nullptr;
 #pragma unroll
   for (int j = 0; j < TM; ++j) {
-    float* crow = C + (long long)(wm * G::WM + j * 32 + l32) * a.c_sm;
+    const int row = wm * G::WM + j * 32 + l32;
+    float* crow = C + (long long)row * a.c_sm;
 #pragma unroll
     for (int i = 0; i < TN; ++i)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
+        const int col = wn * G::WN + i * 32 + 8 * q + 4 * g;
         gr_f32x4 w;
 #pragma unroll
         for (int e = 0; e < 4; ++e) w[e] = gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + e]);
-        *reinterpret_cast<gr_f32x4*>(crow + wn * G::WN + i * 32 + 8 * q + 4 * g) = w;
+        if constexpr ((EPI & GR_EPI_RES) != 0) w += *reinterpret_cast<const gr_f32x4*>(R + (long long)row * a.r_sm + col);
+        *reinterpret_cast<gr_f32x4*>(crow + col) = w;
       }
   }
 }

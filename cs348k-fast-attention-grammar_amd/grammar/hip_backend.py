@@ -259,6 +259,36 @@ def _match_flash32(loop, rl, tile, nb, N, D, causal, scale, qload, ktload, vload
             "scale": scale, "f32": True, "parts": parts}
 
 
+def template_tilings(loop: ParallelLoop, program: Program) -> list:
+    """Output tile shapes at which `loop` lowers to a hand-written template
+    (the flash or the GEMM kernel), whatever its current tiling: the
+    candidates the descent tries as one joint move of the stage's tile dims.
+    Empty for stages no template takes, or pinned to the generic lowering."""
+    if (getattr(loop, "knobs", None) or {}).get("lowering") == "generic":
+        return []
+    out_shape = program.tensors[loop.out]
+    nb = len(out_shape) - 2
+    if nb < 0:
+        return []
+    lead = (1,) * nb
+    cols = GEMM_F32_TILES if program.dtype == "fp32" else tuple(sorted(GEMM_WAVES_N))
+    gemm_rows = GEMM_F32_TILES if program.dtype == "fp32" else tuple(sorted(GEMM_WAVES_M))
+    cands = [lead + (bm, out_shape[-1]) for bm in sorted(FLASH_BM)] + \
+        [lead + (bm, bn) for bm in gemm_rows for bn in cols]
+    keep = loop.tile_shape
+    found = []
+    try:
+        for shape in cands:
+            if any(t > e for t, e in zip(shape, out_shape)) or shape in found:
+                continue
+            loop.tile_shape = shape
+            if _match_flash(loop, program) is not None or _match_gemm(loop, program) is not None:
+                found.append(shape)
+    finally:
+        loop.tile_shape = keep
+    return found
+
+
 def schedule_knobs(loop: ParallelLoop, program: Program) -> dict:
     """The schedule knobs the renderer honours for this stage, each with its
     choices and current value: {name: (choices, current)}; empty for stages
@@ -354,6 +384,7 @@ void {kname}({params}) {{
 # GEMM lowering
 # ---------------------------------------------------------------------------
 GEMM_ACTS = {"relu": 1, "silu": 2}
+GEMM_RES = 4          # epilogue flag: + a residual tensor (GR_EPI_RES)
 GEMM_WAVES_M = {32: 1, 64: 1, 128: 2, 256: 2}
 GEMM_WAVES_N = {32: 1, 64: 1, 128: 2, 256: 2}
 
@@ -394,6 +425,15 @@ def _match_gemm(loop: ParallelLoop, program: Program):
         return None
     st = stores[0]
     x, alpha, act = st.src, 1.0, 0
+    # outermost, optionally: + R, a tensor loaded at the output's own indices
+    # (a residual add, fused as the GR_EPI_RES epilogue)
+    res = resadd = None
+    if isinstance(x, Compute) and x.op == "add" and len(x.inputs) == 2:
+        for r_, other in ((x.inputs[1], x.inputs[0]), (x.inputs[0], x.inputs[1])):
+            if isinstance(r_, Load) and r_.index == st.index and r_.source != loop.out and \
+                    tuple(program.tensors[r_.source]) == tuple(program.tensors[loop.out]):
+                res, resadd, x = r_, x, other
+                break
     chain = []
     while isinstance(x, Compute) and x.op in ("mulc", "relu", "silu"):
         chain.append(x)
@@ -423,6 +463,9 @@ def _match_gemm(loop: ParallelLoop, program: Program):
     if not (isinstance(aload, Load) and isinstance(bload, Load)):
         return None
     allowed = {id(st), id(mm), id(aload), id(bload)} | {id(c) for c in chain}
+    if res is not None:
+        allowed |= {id(res), id(resadd)}
+        act |= GEMM_RES
     if rl is not None:
         allowed.add(id(rl))
         if rl.axis != _contraction_axis(mm):
@@ -476,7 +519,8 @@ def _match_gemm(loop: ParallelLoop, program: Program):
         return {"a": aload.source, "b": bload.source, "c": loop.out, "M": M, "N": N, "K": K, "batch": batch,
                 "a_sb": M * K if a_batched else 0, "b_sb": K * N if b_batched else 0, "c_sb": M * N,
                 "kmajor": kmajor, "act": act, "alpha": alpha, "BM": BM, "BN": BN, "BK": BK,
-                "WGM": 2 if BM >= 64 else 1, "WGN": 2 if BN >= 64 else 1, "f32": True}
+                "WGM": 2 if BM >= 64 else 1, "WGN": 2 if BN >= 64 else 1, "f32": True,
+                "res": res.source if res is not None else None}
     if BM not in GEMM_WAVES_M or BN not in GEMM_WAVES_N:   # ragged M, N: edge tiles store their valid part
         return None
     BK = rl.tile if rl is not None else 64
@@ -491,7 +535,8 @@ def _match_gemm(loop: ParallelLoop, program: Program):
     wgm, wgn = _gemm_waves(BM, BN)
     return {"a": aload.source, "b": bload.source, "c": loop.out, "M": M, "N": N, "K": K, "batch": batch,
             "a_sb": M * K if a_batched else 0, "b_sb": K * N if b_batched else 0, "c_sb": M * N,
-            "kmajor": kmajor, "act": act, "alpha": alpha, "BM": BM, "BN": BN, "BK": BK, "WGM": wgm, "WGN": wgn}
+            "kmajor": kmajor, "act": act, "alpha": alpha, "BM": BM, "BN": BN, "BK": BK, "WGM": wgm, "WGN": wgn,
+            "res": res.source if res is not None else None}
 
 
 def _render_gemm(loop, program, f) -> tuple:
@@ -500,6 +545,8 @@ def _render_gemm(loop, program, f) -> tuple:
     args = _loop_tensors(loop)
     params = ", ".join(f"{'const ' if a != loop.out else ''}{T}* __restrict__ {_cname(a)}" for a in args)
     km = "true" if f["kmajor"] else "false"
+    res_line = (f"\n  a.r = {_cname(f['res'])}; a.r_sb = {f['c_sb']}LL; a.r_sm = {f['N']};"
+                if f.get("res") else "")
     if f.get("f32"):
         nt = f["WGM"] * f["WGN"] * 64
         code = f"""
@@ -513,7 +560,7 @@ void {kname}({params}) {{
   a.b_sb = {f['b_sb']}LL; a.b_s = {f['K'] if f['kmajor'] else f['N']};
   a.c_sb = {f['c_sb']}LL; a.c_sm = {f['N']};
   a.M = {f['M']}; a.N = {f['N']}; a.K = {f['K']};
-  a.alpha = {_flt(f['alpha'])};
+  a.alpha = {_flt(f['alpha'])};{res_line}
   gr_gemm_f32_body<{f['BM']}, {f['BN']}, {f['BK']}, {f['WGM']}, {f['WGN']}, {km}, {f['act']}>(a, gr_gemm_smem);
 }}
 """
@@ -535,7 +582,7 @@ void {kname}({params}) {{
   a.b_sb = {f['b_sb']}LL; a.b_s = {f['K'] if f['kmajor'] else f['N']};
   a.c_sb = {f['c_sb']}LL; a.c_sm = {f['N']};
   a.M = {f['M']}; a.N = {f['N']}; a.K = {f['K']};
-  a.alpha = {_flt(f['alpha'])};
+  a.alpha = {_flt(f['alpha'])};{res_line}
   gr_gemm_body<{tpl}>(a, gr_gemm_smem);
 }}
 """

@@ -118,3 +118,54 @@ def test_descent_can_reach_flash_structure_under_proxy():
     labels = [r.label for r in O.enumerate_rewrites(q, O.DEFAULT_RULES)]
     assert "subtile(softmax_matmul,j)" in labels
     assert "split_softmax" in labels
+
+
+def test_stage1_reaches_template_tilings_in_one_move():
+    """A stage that lowers to the GEMM only when both its tile dims are in the
+    GEMM's set (here the LN block's r = a @ W2 + X at 16 x 16, generic) is
+    moved there by Stage 1's template snaps, which a one-coordinate sweep
+    cannot do when every single-dim move keeps the generic lowering."""
+    import run_mlp_search as RM
+    from grammar import rewrites as R
+    from grammar.hip_backend import template_tilings, parse_plan
+    from grammar.kernel_ast import emit_module
+    from grammar.optimization import stage1_sweep
+    p = RM.build_mlp_ln(256, 512, 1024)
+    p = R.merge(p, p.body[2], p.body[3])
+    p = R.merge(p, p.body[0], p.body[1])
+    for l in p.body[:2]:
+        l.tile_shape = (16, 16)
+    r = p.body[1]
+    shapes = template_tilings(r, p)
+    assert (64, 64) in shapes and (32, 128) in shapes and (16, 16) not in shapes
+
+    class Lowering:
+        """Score: 1 per generic stage, 0.1 per template stage: every
+        single-dim move from 16 x 16 keeps stage r generic and scores the same."""
+        def __init__(self):
+            self.seen = 0
+
+        def prefetch(self, programs):
+            pass
+
+        def __call__(self, prog):
+            self.seen += 1
+            try:
+                steps = parse_plan(emit_module(prog))["steps"]
+            except Exception:
+                return 1e9                        # over LDS or not renderable: a penalty
+
+            return sum(0.1 if s["lowering"] in ("gemm", "flash") else 1.0 for s in steps)
+
+    import grammar.optimization as O
+    out, _ = stage1_sweep(p, Lowering(), ladder=(16, 32, 64, 128, 256))
+    lowerings = [s["lowering"] for s in parse_plan(emit_module(out))["steps"]]
+    assert lowerings[:2] == ["gemm", "gemm"], lowerings
+    # without the snaps the sweep stays on the generic lowering
+    keep = O._template_snaps
+    O._template_snaps = lambda work, params, ev, loss: loss
+    try:
+        out, _ = stage1_sweep(p, Lowering(), ladder=(16, 32, 64, 128, 256))
+    finally:
+        O._template_snaps = keep
+    assert [s["lowering"] for s in parse_plan(emit_module(out))["steps"]][:2] == ["generic", "generic"]

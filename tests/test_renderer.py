@@ -162,3 +162,20 @@ def test_lds_overflow_is_reported():
     pw = Program({"x": (512, 512), "o": (512, 512)},
                  [ParallelLoop("o", (256, 512), ("n", "m"), [y, rl, Store("o", rl, ["n", "m"])])])
     assert parse_plan(render_module(pw))["steps"][0]["lowering"] == "rows"
+
+
+def test_residual_add_lowers_to_the_gemm_epilogue():
+    """A stage computing A @ B + R (R loaded at the output's indices) lowers to
+    the GEMM with the residual epilogue flag (GR_EPI_RES = 4) and R's
+    pointer and strides in the argument block; an add of anything else keeps
+    the generic lowering."""
+    import run_mlp_search as RM
+    from grammar import rewrites as R
+    for dt, body in (("fp32", "gr_gemm_f32_body<64, 64, 32, 2, 2, false, 4>"),
+                     ("fp16", "gr_gemm_body<_Float16, 64, 64, 64, 1, 1, false, 4>")):
+        p = RM.build_mlp_ln(256, 512, 1024, tile=64, dtype=dt)
+        p = R.merge(p, p.body[2], p.body[3])
+        src = emit_module(p)
+        st = [s for s in parse_plan(src)["steps"] if s["kernel"] == "t_r_kernel"][0]
+        assert st["lowering"] == "gemm" and "t_X" in src.split("void t_r_kernel(")[1].split(")")[0]
+        assert "a.r = t_X; a.r_sb = 131072LL; a.r_sm = 512;" in src and body in src, dt

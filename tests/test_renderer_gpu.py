@@ -284,6 +284,41 @@ def test_ln_mlp_block_on_gpu(tile, sk):
     assert np.allclose(got, want, rtol=1e-3, atol=1e-3)
 
 
+@pytest.mark.parametrize("dt", ["fp32", "fp16", "bf16"])
+def test_residual_add_fuses_into_the_gemm(dt):
+    """The LN block with its second matmul and the residual add merged into one
+    stage (r = a @ W2 + X) and the first with its relu (a = relu(X @ W1)):
+    both lower to the GEMM, the residual read in its epilogue (GR_EPI_RES)
+    and added in fp32 before the output is rounded. Against the tile
+    interpreter on the same (rounded) inputs."""
+    _cuda()
+    import run_mlp_search as RM
+    from grammar import rewrites as R
+    from grammar.hip_module import load_module
+    p = RM.build_mlp_ln(256, 256, 512, tile=64, dtype=dt)
+    p = R.merge(p, p.body[2], p.body[3])
+    p = R.merge(p, p.body[0], p.body[1])
+    mod = load_module(emit_module(p))
+    assert [s["lowering"] for s in mod.plan["steps"]] == ["gemm", "gemm", "rows"]
+    ins = {k: v.float().cpu().numpy() for k, v in RM.mlp_inputs(256, 256, 512, dt, seed=3).items()}
+    args = [torch.from_numpy(ins[n]).to(_cuda()).to(mod.dtype) for n in mod.inputs]
+    tensors = mod.run_with(args)
+    torch.cuda.synchronize()
+    if dt == "fp32":
+        want = run_program(p, ins)
+        tol = 1e-3
+    else:
+        rnd = (lambda x: np.asarray(x, dtype=np.float16).astype(np.float32)) if dt == "fp16" else \
+            (lambda x: torch.from_numpy(np.asarray(x, dtype=np.float32)).bfloat16().float().numpy())
+        want = run_program(p, ins, storage_round=rnd)
+        tol = 2e-2 if dt == "bf16" else 5e-3
+    for name in ("r", "out"):
+        got = tensors[name].float().cpu().numpy()
+        err = float(np.max(np.abs(got - want[name])))
+        print(f"[residual-gemm] {dt} {name}: max|d| {err:.2e}", flush=True)
+        assert np.isfinite(got).all() and err <= tol * max(1.0, float(np.max(np.abs(want[name]))))
+
+
 @pytest.mark.parametrize("dt,causal,merges", [("fp16", False, 0), ("bf16", True, 0), ("fp16", False, 3)])
 def test_row_lowered_softmax_stages(dt, causal, merges):
     """The softmax stages of the atomic attention program (scale, causal
