@@ -3,14 +3,9 @@
 
 // generated from a grammar program: 1 stage(s), storage fp32
 
-// stage O: fp32 flash attention on the fp32 matrix cores (32 queries x 2 chunk(s) of 64 keys
-// per workgroup, one chunk per wave, merged in LDS; 4 workgroup(s) per query block)
-// partials of the 4 workgroups of each query block, merged by the last of them;
-// they are this module's, so two launches of it must not overlap
-__device__ float gr_ws_t_O[131072];
-__device__ float gr_ml_t_O[4096];
-__device__ unsigned int gr_cnt_t_O[16];
-extern "C" __global__ __launch_bounds__(128)
+// stage O: fp32 flash attention on the fp32 matrix cores (32 queries x 4 chunk(s) of 128 keys
+// per workgroup, one chunk per wave, merged in LDS; 1 workgroup(s) per query block)
+extern "C" __global__ __launch_bounds__(256)
 void t_O_kernel(const float* __restrict__ t_Q, const float* __restrict__ t_KT, const float* __restrict__ t_V, float* __restrict__ t_O) {
   extern __shared__ __attribute__((aligned(16))) char gr_flash_smem[];
   gr_attn_args a;
@@ -21,7 +16,7 @@ void t_O_kernel(const float* __restrict__ t_Q, const float* __restrict__ t_KT, c
   a.o_sb = 32768LL; a.o_sh = 0; a.o_sn = 64;
   a.B = 1; a.H = 1; a.N = 512; a.Nq = 512;
   a.scale_log2 = 0.18033688011112042f;
-  gr_flash32_fwd_body<64, 64, 2, true, 4>(a, gr_flash_smem, gr_ws_t_O, gr_ml_t_O, gr_cnt_t_O);
+  gr_flash32_fwd_body<64, 128, 4, true, 1>(a, gr_flash_smem, nullptr, nullptr, nullptr);
 }
 
-/*GR_PLAN {"dtype": "fp32", "fn": "fn", "inputs": ["KT", "Q", "V"], "intermediates": [], "meta": {"dtype": "fp32", "flops": 68681728, "flops_exact": true, "inputs": [["KT", [64, 512]], ["Q", [512, 64]], ["V", [512, 64]]], "output": ["O", [512, 64]]}, "outputs": ["O"], "steps": [{"args": ["Q", "KT", "V", "O"], "block": [128, 1, 1], "grid": [64, 1, 1], "kernel": "t_O_kernel", "lds": 17936, "lowering": "flash", "tiles": {"block_m": 64, "block_n": 64, "parts": 4, "waves": 2}}], "tensors": {"KT": [64, 512], "O": [512, 64], "Q": [512, 64], "V": [512, 64]}} GR_PLAN*/
+/*GR_PLAN {"dtype": "fp32", "fn": "fn", "inputs": ["KT", "Q", "V"], "intermediates": [], "meta": {"dtype": "fp32", "flops": 68681728, "flops_exact": true, "inputs": [["KT", [64, 512]], ["Q", [512, 64]], ["V", [512, 64]]], "output": ["O", [512, 64]]}, "outputs": ["O"], "steps": [{"args": ["Q", "KT", "V", "O"], "block": [256, 1, 1], "grid": [16, 1, 1], "kernel": "t_O_kernel", "lds": 35856, "lowering": "flash", "tiles": {"block_m": 128, "block_n": 128, "parts": 1, "waves": 4}}], "tensors": {"KT": [64, 512], "O": [512, 64], "Q": [512, 64], "V": [512, 64]}} GR_PLAN*/

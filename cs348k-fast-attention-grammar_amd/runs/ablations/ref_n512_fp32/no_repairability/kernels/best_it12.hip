@@ -6,7 +6,7 @@
 // stage O: fp32 flash attention on the fp32 matrix cores (32 queries x 4 chunk(s) of 128 keys
 // per workgroup, one chunk per wave, merged in LDS; 1 workgroup(s) per query block)
 extern "C" __global__ __launch_bounds__(256)
-void t_O_kernel(const float* __restrict__ t_KT, const float* __restrict__ t_Q, const float* __restrict__ t_V, float* __restrict__ t_O) {
+void t_O_kernel(const float* __restrict__ t_Q, const float* __restrict__ t_KT, const float* __restrict__ t_V, float* __restrict__ t_O) {
   extern __shared__ __attribute__((aligned(16))) char gr_flash_smem[];
   gr_attn_args a;
   a.q = t_Q; a.k = t_KT; a.v = t_V; a.o = t_O;
@@ -19,4 +19,4 @@ void t_O_kernel(const float* __restrict__ t_KT, const float* __restrict__ t_Q, c
   gr_flash32_fwd_body<64, 128, 4, true, 1>(a, gr_flash_smem, nullptr, nullptr, nullptr);
 }
 
-/*GR_PLAN {"dtype": "fp32", "fn": "fn", "inputs": ["KT", "Q", "V"], "intermediates": [], "meta": {"dtype": "fp32", "flops": 68681728, "flops_exact": true, "inputs": [["KT", [64, 512]], ["Q", [512, 64]], ["V", [512, 64]]], "output": ["O", [512, 64]]}, "outputs": ["O"], "steps": [{"args": ["KT", "Q", "V", "O"], "block": [256, 1, 1], "grid": [16, 1, 1], "kernel": "t_O_kernel", "lds": 35856, "lowering": "flash", "tiles": {"block_m": 128, "block_n": 128, "parts": 1, "waves": 4}}], "tensors": {"KT": [64, 512], "O": [512, 64], "Q": [512, 64], "V": [512, 64]}} GR_PLAN*/
+/*GR_PLAN {"dtype": "fp32", "fn": "fn", "inputs": ["KT", "Q", "V"], "intermediates": [], "meta": {"dtype": "fp32", "flops": 68681728, "flops_exact": true, "inputs": [["KT", [64, 512]], ["Q", [512, 64]], ["V", [512, 64]]], "output": ["O", [512, 64]]}, "outputs": ["O"], "steps": [{"args": ["Q", "KT", "V", "O"], "block": [256, 1, 1], "grid": [16, 1, 1], "kernel": "t_O_kernel", "lds": 35856, "lowering": "flash", "tiles": {"block_m": 128, "block_n": 128, "parts": 1, "waves": 4}}], "tensors": {"KT": [64, 512], "O": [512, 64], "Q": [512, 64], "V": [512, 64]}} GR_PLAN*/

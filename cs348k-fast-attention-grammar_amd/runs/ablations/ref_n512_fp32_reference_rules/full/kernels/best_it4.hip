@@ -1,42 +1,19 @@
 #include "gr_gemm_f32.h"
 
 // generated from a grammar program: 7 stage(s), storage fp32
-// stage S: generic LDS-tile kernel, tile (16, 16), 9216 B LDS
-extern "C" __global__ __launch_bounds__(256) void t_S_kernel(const float* __restrict__ t_Q, const float* __restrict__ t_KT, float* __restrict__ t_S) {
-  extern __shared__ __attribute__((aligned(16))) float gr_lds[];
-  constexpr int B0 = 0;
-  constexpr int B1 = 1024;
-  constexpr int B2 = 2048;
-  int bid = blockIdx.x;
-  const int b_t_j = bid % 32; bid /= 32;
-  const int b_t_i = bid % 32; bid /= 32;
-  for (int e = threadIdx.x; e < 1024; e += 256) {
-    const int i0 = (e / 64);
-    const int i1 = e % 64;
-    gr_lds[B0 + e] = (float)t_Q[(long long)((b_t_i)*16 + i0)*64 + (long long)(i1)];
-  }
-  __syncthreads();
-  for (int e = threadIdx.x; e < 1024; e += 256) {
-    const int i0 = (e / 16);
-    const int i1 = e % 16;
-    gr_lds[B1 + e] = (float)t_KT[(long long)(i0)*512 + (long long)((b_t_j)*16 + i1)];
-  }
-  __syncthreads();
-  // matmul: C = A @ B (K = 64)
-  for (int e = threadIdx.x; e < 256; e += 256) {
-    const int i0 = (e / 16);
-    const int i1 = e % 16;
-    float s = 0.f;
-    for (int k = 0; k < 64; ++k) s = fmaf(gr_lds[B0 + (i0)*64 + (k)], gr_lds[B1 + (k)*16 + (i1)], s);
-    gr_lds[B2 + e] = s;
-  }
-  __syncthreads();
-  for (int e = threadIdx.x; e < 256; e += 256) {
-    const int i0 = (e / 16);
-    const int i1 = e % 16;
-    t_S[(long long)((b_t_i)*16 + i0)*512 + (long long)((b_t_j)*16 + i1)] = (float)gr_lds[B2 + (i0)*16 + (i1)];
-  }
-  __syncthreads();
+
+// stage S: fp32 MFMA GEMM 512x512x64 (x1), tile 32x64x32
+extern "C" __global__ __launch_bounds__(128)
+void t_S_kernel(const float* __restrict__ t_Q, const float* __restrict__ t_KT, float* __restrict__ t_S) {
+  extern __shared__ __attribute__((aligned(16))) char gr_gemm_smem[];
+  gr_gemm_args a;
+  a.a = t_Q; a.b = t_KT; a.c = t_S;
+  a.a_sb = 32768LL; a.a_sm = 64;
+  a.b_sb = 32768LL; a.b_s = 512;
+  a.c_sb = 262144LL; a.c_sm = 512;
+  a.M = 512; a.N = 512; a.K = 64;
+  a.alpha = 1.0f;
+  gr_gemm_f32_body<32, 64, 32, 1, 2, false, 0>(a, gr_gemm_smem);
 }
 
 
@@ -142,4 +119,4 @@ void t_O_kernel(const float* __restrict__ t_P, const float* __restrict__ t_V, fl
   gr_gemm_f32_body<32, 32, 32, 1, 1, false, 0>(a, gr_gemm_smem);
 }
 
-/*GR_PLAN {"dtype": "fp32", "fn": "fn", "inputs": ["KT", "Q", "V"], "intermediates": ["P", "S", "Ss", "e", "mx", "sm"], "meta": {"dtype": "fp32", "flops": 68681728, "flops_exact": true, "inputs": [["KT", [64, 512]], ["Q", [512, 64]], ["V", [512, 64]]], "output": ["O", [512, 64]]}, "outputs": ["O"], "steps": [{"args": ["Q", "KT", "S"], "block": [256, 1, 1], "grid": [1024, 1, 1], "kernel": "t_S_kernel", "lds": 9216, "lowering": "generic"}, {"args": ["S", "Ss"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_Ss_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["Ss", "mx"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_mx_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["Ss", "mx", "e"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_e_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["e", "sm"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_sm_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["e", "sm", "P"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_P_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["P", "V", "O"], "block": [64, 1, 1], "grid": [32, 1, 1], "kernel": "t_O_kernel", "lds": 19456, "lowering": "gemm", "tiles": {"block_k": 32, "block_m": 32, "block_n": 32}}], "tensors": {"KT": [64, 512], "O": [512, 64], "P": [512, 512], "Q": [512, 64], "S": [512, 512], "Ss": [512, 512], "V": [512, 64], "e": [512, 512], "mx": [512, 1], "sm": [512, 1]}} GR_PLAN*/
+/*GR_PLAN {"dtype": "fp32", "fn": "fn", "inputs": ["KT", "Q", "V"], "intermediates": ["P", "S", "Ss", "e", "mx", "sm"], "meta": {"dtype": "fp32", "flops": 68681728, "flops_exact": true, "inputs": [["KT", [64, 512]], ["Q", [512, 64]], ["V", [512, 64]]], "output": ["O", [512, 64]]}, "outputs": ["O"], "steps": [{"args": ["Q", "KT", "S"], "block": [128, 1, 1], "grid": [128, 1, 1], "kernel": "t_S_kernel", "lds": 27648, "lowering": "gemm", "tiles": {"block_k": 32, "block_m": 32, "block_n": 64}}, {"args": ["S", "Ss"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_Ss_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["Ss", "mx"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_mx_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["Ss", "mx", "e"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_e_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["e", "sm"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_sm_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["e", "sm", "P"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_P_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["P", "V", "O"], "block": [64, 1, 1], "grid": [32, 1, 1], "kernel": "t_O_kernel", "lds": 19456, "lowering": "gemm", "tiles": {"block_k": 32, "block_m": 32, "block_n": 32}}], "tensors": {"KT": [64, 512], "O": [512, 64], "P": [512, 512], "Q": [512, 64], "S": [512, 512], "Ss": [512, 512], "V": [512, 64], "e": [512, 512], "mx": [512, 1], "sm": [512, 1]}} GR_PLAN*/
