@@ -420,7 +420,7 @@ def bench_module(path: str, steps: int, warmup: int, seed: int) -> dict:
     return {"metric": "module TFLOP/s (KERNEL_META flops)", "module": path, "value": round(flops / (ms * 1e-3) / 1e12, 3),
             "unit": "TFLOP/s", "ms_per_step": round(ms, 6), "steps": steps, "warmup": warmup,
             "clock_ramp_ms": CLOCK_RAMP_MS, "flops": flops, "flops_exact": meta.get("flops_exact"),
-            "dtype": mod.plan["dtype"], "stages": len(mod.plan["steps"]),
+            "dtype": mod.plan["dtype"], "stages": len([st for st in mod.plan["steps"] if not st.get("merge")]),
             "lowering": [st["lowering"] for st in mod.plan["steps"]], "check": check}
 
 

@@ -1,7 +1,7 @@
 // gr_flash_f32.h -- fp32 attention forward on the fp32 matrix cores of gfx950
-// (v_mfma_f32_32x32x2_f32), for the grammar's fp32 programs: one launch, keys
-// split over waves and workgroups, partials merged in LDS and then by the
-// last workgroup of each query block.
+// (v_mfma_f32_32x32x2_f32), for the grammar's fp32 programs: keys split over
+// the waves of a workgroup (merged in LDS) and, optionally, over workgroups
+// (merged by a second launch).
 //
 //   O = softmax(scale * Q K^T) V      Q, V, O [B, H, N, D], K natural or K^T
 //
@@ -14,12 +14,11 @@
 // memory into registers (the next block's loads in flight during this
 // block's MFMAs). The NW partials (O, m, l) are merged through LDS, each wave
 // merging a D / NW slice. With PARTS = N / (NW BN) > 1 workgroups per query
-// block, each leaves its merged partial in a workspace and the last one to
-// finish (a device-scope counter) merges them,
-//   O = sum_s 2^((m_s - M) c) O_s / sum_s 2^((m_s - M) c) l_s,  M = max_s m_s,
-// and resets the counter for the next launch. Workspace and counters are
-// module-scope device arrays the renderer sizes for the stage (zero at load);
-// two launches of one module must not overlap.
+// block, each leaves its merged partial in a workspace and a second launch
+// (gr_flash32_merge_body) combines them,
+//   O = sum_s 2^((m_s - M) c) O_s / sum_s 2^((m_s - M) c) l_s,  M = max_s m_s.
+// The workspace is module-scope device arrays the renderer sizes for the
+// stage; two launches of one module must not overlap.
 //
 //  * Transposed form as in gr_flash_fwd_body: S^T = K Q^T, O^T = V^T P^T. A
 //    32x32x2 MFMA contracts one index per half-wave: for d the lane of half g
@@ -36,12 +35,11 @@ template <int D, int NW>
 struct gr_flash32_lds {
   static constexpr int LD = D + 4;                       // padded row of a wave's O partial (floats)
   static constexpr int O_FLOATS = NW * 32 * LD;
-  static constexpr int BYTES = (O_FLOATS + NW * 32 * 2) * 4 + 16;
+  static constexpr int BYTES = (O_FLOATS + NW * 32 * 2) * 4;
 };
 
 template <int D, int BN, int NW, bool KT_LAYOUT, int PARTS>
-__device__ __forceinline__ void gr_flash32_fwd_body(const gr_attn_args& a, char* lds, float* ws_o, float* ws_ml,
-                                                    unsigned int* cnt) {
+__device__ __forceinline__ void gr_flash32_fwd_body(const gr_attn_args& a, char* lds, float* ws_o, float* ws_ml) {
   constexpr int KB = BN / 32;      // 32-key blocks per wave
   constexpr int DB = D / 32;       // 32-wide head-dim blocks of O^T
   constexpr int DG = D / 8;        // groups of 8 d (4 MFMAs of 2)
@@ -147,7 +145,6 @@ __device__ __forceinline__ void gr_flash32_fwd_body(const gr_attn_args& a, char*
   // consecutive queries fall on distinct banks
   float* lo = reinterpret_cast<float*>(lds);
   float* lml = lo + L::O_FLOATS;
-  unsigned int* lflag = reinterpret_cast<unsigned int*>(lml + NW * 32 * 2);
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -200,10 +197,8 @@ __device__ __forceinline__ void gr_flash32_fwd_body(const gr_attn_args& a, char*
   };
   if constexpr (PARTS == 1) {
     store_o(L_);
-    return;
   } else {
-    // this workgroup's merged partial -> workspace; the last workgroup of the
-    // query block merges them all
+    // this workgroup's merged partial -> workspace, for gr_flash32_merge_body
     const long long row = (long long)(part * lead + bh) * a.N + q0 + l32;
     float* wo = ws_o + row * D + d0;
 #pragma unroll
@@ -212,39 +207,45 @@ __device__ __forceinline__ void gr_flash32_fwd_body(const gr_attn_args& a, char*
       *reinterpret_cast<gr_f32x4*>(wo + 16 * p + 4) = (gr_f32x4){acc[p][4], acc[p][5], acc[p][6], acc[p][7]};
     }
     if (wave == 0 && g == 0) *reinterpret_cast<gr_f32x2*>(ws_ml + row * 2) = (gr_f32x2){mx, L_};
-    __threadfence();   // this thread's partial is visible device-wide before it is counted
-    __syncthreads();
-    if (tid == 0) *lflag = atomicAdd(cnt + (long long)bh * nqb + qblk, 1u);
-    __syncthreads();
-    if (*lflag != (unsigned int)(PARTS - 1)) return;
-    __threadfence();   // every counted partial is visible to this workgroup
-    float gm = -GR_INF;
-#pragma unroll
-    for (int s = 0; s < PARTS; ++s) gm = fmaxf(gm, ws_ml[((long long)(s * lead + bh) * a.N + q0 + l32) * 2]);
-#pragma unroll
-    for (int p = 0; p < PER; ++p)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[p][e] = 0.f;
-    float GL = 0.f;
-#pragma unroll
-    for (int s = 0; s < PARTS; ++s) {
-      const long long r2 = (long long)(s * lead + bh) * a.N + q0 + l32;
-      const gr_f32x2 ml = *reinterpret_cast<const gr_f32x2*>(ws_ml + r2 * 2);
-      const float e = gr_exp2((ml[0] - gm) * c);
-      GL = fmaf(e, ml[1], GL);
-#pragma unroll
-      for (int p = 0; p < PER; ++p) {
-        const float* src = ws_o + r2 * D + d0 + 16 * p;
-        const gr_f32x4 v0 = *reinterpret_cast<const gr_f32x4*>(src);
-        const gr_f32x4 v1 = *reinterpret_cast<const gr_f32x4*>(src + 4);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc[p][i] = fmaf(e, v0[i], acc[p][i]);
-          acc[p][4 + i] = fmaf(e, v1[i], acc[p][4 + i]);
-        }
-      }
-    }
-    store_o(GL);
-    if (tid == 0) cnt[(long long)bh * nqb + qblk] = 0u;   // ready for the next launch
   }
+}
+
+// The second launch of a split stage: O from the PARTS partials of every
+// query, O = sum_s 2^((m_s - M) c) O_s / sum_s 2^((m_s - M) c) l_s with
+// M = max_s m_s. One thread per (query row, 8 head dims); the grid covers
+// lead * N * D / 8 threads in workgroups of 256.
+template <int D, int PARTS>
+__device__ __forceinline__ void gr_flash32_merge_body(const gr_attn_args& a, const float* ws_o, const float* ws_ml) {
+  constexpr int CH = D / 8;
+  const int lead = a.B * a.H;
+  const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long rows = (long long)lead * a.N;
+  if (idx >= rows * CH) return;
+  const int ch = (int)(idx % CH);
+  const long long r = idx / CH;                     // bh * N + q
+  const int bh = (int)(r / a.N), q = (int)(r % a.N);
+  const float c = a.scale_log2;
+  float mx = -GR_INF;
+#pragma unroll
+  for (int s = 0; s < PARTS; ++s) mx = fmaxf(mx, ws_ml[((long long)s * rows + r) * 2]);
+  float L = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < PARTS; ++s) {
+    const gr_f32x2 ml = *reinterpret_cast<const gr_f32x2*>(ws_ml + ((long long)s * rows + r) * 2);
+    const float w = gr_exp2((ml[0] - mx) * c);
+    L = fmaf(w, ml[1], L);
+    const float* src = ws_o + ((long long)s * rows + r) * D + ch * 8;
+    const gr_f32x4 v0 = *reinterpret_cast<const gr_f32x4*>(src);
+    const gr_f32x4 v1 = *reinterpret_cast<const gr_f32x4*>(src + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc[e] = fmaf(w, v0[e], acc[e]);
+      acc[4 + e] = fmaf(w, v1[e], acc[4 + e]);
+    }
+  }
+  const float inv = 1.0f / L;
+  const int b = bh / a.H, h = bh % a.H;
+  float* dst = (float*)a.o + b * a.o_sb + h * a.o_sh + (long long)q * a.o_sn + ch * 8;
+  *reinterpret_cast<gr_f32x4*>(dst) = (gr_f32x4){acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+  *reinterpret_cast<gr_f32x4*>(dst + 4) = (gr_f32x4){acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv};
 }

@@ -303,42 +303,55 @@ def schedule_knobs(loop: ParallelLoop, program: Program) -> dict:
 
 
 def _render_flash32(loop, program, f) -> tuple:
+    """The fp32 flash stage: one kernel, or with PARTS > 1 workgroups per
+    query block a second one that merges their partials (two plan steps)."""
     kname = f"{_cname(loop.out)}_kernel"
     args = _loop_tensors(loop)
     params = ", ".join(f"{'const ' if a != loop.out else ''}float* __restrict__ {_cname(a)}" for a in args)
     N, D, lead, parts, nw = f["N"], f["D"], f["lead"], f["parts"], f["NW"]
     ws = _cname(loop.out)
-    if parts > 1:
-        arrays = (f"// partials of the {parts} workgroups of each query block, merged by the last of them;\n"
-                  f"// they are this module's, so two launches of it must not overlap\n"
-                  f"__device__ float gr_ws_{ws}[{parts * lead * N * D}];\n"
-                  f"__device__ float gr_ml_{ws}[{parts * lead * N * 2}];\n"
-                  f"__device__ unsigned int gr_cnt_{ws}[{lead * N // 32}];\n")
-        ptrs = f"gr_ws_{ws}, gr_ml_{ws}, gr_cnt_{ws}"
-    else:
-        arrays, ptrs = "", "nullptr, nullptr, nullptr"
-    code = f"""
-// stage {loop.out}: fp32 flash attention on the fp32 matrix cores (32 queries x {nw} chunk(s) of {f['BN']} keys
-// per workgroup, one chunk per wave, merged in LDS; {parts} workgroup(s) per query block)
-{arrays}extern "C" __global__ __launch_bounds__({nw * 64})
-void {kname}({params}) {{
-  extern __shared__ __attribute__((aligned(16))) char gr_flash_smem[];
-  gr_attn_args a;
+    setup = f"""  gr_attn_args a;
   a.q = {_cname(f['q'])}; a.k = {_cname(f['kt'])}; a.v = {_cname(f['v'])}; a.o = {_cname(f['o'])};
   a.q_sb = {N * D}LL; a.q_sh = 0; a.q_sn = {D};
   a.k_sb = {N * D}LL; a.k_sh = 0; a.k_sn = {N};
   a.v_sb = {N * D}LL; a.v_sh = 0; a.v_sn = {D};
   a.o_sb = {N * D}LL; a.o_sh = 0; a.o_sn = {D};
   a.B = {lead}; a.H = 1; a.N = {N}; a.Nq = {N};
-  a.scale_log2 = {_flt(f['scale'] * LOG2E)};
+  a.scale_log2 = {_flt(f['scale'] * LOG2E)};"""
+    if parts > 1:
+        arrays = (f"// partials of the {parts} workgroups of each query block, merged by {kname[:-7]}_merge_kernel;\n"
+                  f"// they are this module's, so two launches of it must not overlap\n"
+                  f"__device__ float gr_ws_{ws}[{parts * lead * N * D}];\n"
+                  f"__device__ float gr_ml_{ws}[{parts * lead * N * 2}];\n")
+        ptrs = f"gr_ws_{ws}, gr_ml_{ws}"
+    else:
+        arrays, ptrs = "", "nullptr, nullptr"
+    code = f"""
+// stage {loop.out}: fp32 flash attention on the fp32 matrix cores (32 queries x {nw} chunk(s) of {f['BN']} keys
+// per workgroup, one chunk per wave, merged in LDS; {parts} workgroup(s) per query block)
+{arrays}extern "C" __global__ __launch_bounds__({nw * 64})
+void {kname}({params}) {{
+  extern __shared__ __attribute__((aligned(16))) char gr_flash_smem[];
+{setup}
   gr_flash32_fwd_body<{D}, {f['BN']}, {nw}, true, {parts}>(a, gr_flash_smem, {ptrs});
 }}
 """
     grid = lead * (N // 32) * parts
-    lds = (nw * 32 * (D + 4) + nw * 32 * 2) * 4 + 16          # gr_flash32_lds<D, NW>::BYTES
-    return code, {"kernel": kname, "grid": [grid, 1, 1], "block": [nw * 64, 1, 1], "lds": lds,
-                  "args": args, "lowering": "flash",
-                  "tiles": {"block_m": f["BM"], "block_n": f["BN"], "waves": nw, "parts": parts}}
+    lds = (nw * 32 * (D + 4) + nw * 32 * 2) * 4          # gr_flash32_lds<D, NW>::BYTES
+    steps = [{"kernel": kname, "grid": [grid, 1, 1], "block": [nw * 64, 1, 1], "lds": lds,
+              "args": args, "lowering": "flash",
+              "tiles": {"block_m": f["BM"], "block_n": f["BN"], "waves": nw, "parts": parts}}]
+    if parts > 1:
+        mname = f"{kname[:-7]}_merge_kernel"
+        code += f"""extern "C" __global__ __launch_bounds__(256)
+void {mname}({params}) {{
+{setup}
+  gr_flash32_merge_body<{D}, {parts}>(a, gr_ws_{ws}, gr_ml_{ws});
+}}
+"""
+        steps.append({"kernel": mname, "grid": [_cdiv(lead * N * (D // 8), 256), 1, 1], "block": [256, 1, 1],
+                      "lds": 0, "args": args, "lowering": "flash", "merge": True})
+    return code, steps
 
 
 def _render_flash(loop, program, f) -> tuple:
@@ -1482,7 +1495,7 @@ def render_module(program: Program, fn_name: str = "fn", check: bool = False) ->
             excess += e.need
             continue
         parts.append(code)
-        steps.append(step)
+        steps.extend(step if isinstance(step, list) else [step])
     if over:
         raise LdsOverflow(",".join(over), excess)
     plan = {"fn": fn_name, "dtype": program.dtype, "inputs": inputs, "intermediates": inter, "outputs": outputs,

@@ -90,14 +90,17 @@ def test_flash_lowering_selected_for_fp16_flash_structure():
     # (block_n keys per wave), its partials in module-scope device arrays
     p32 = C.p_flash_attention(B=2, H=2, N=256, d=64, bm=64, bn=32, dtype="fp32")
     src32 = emit_module(p32)
-    st = parse_plan(src32)["steps"][0]
+    st, mg = parse_plan(src32)["steps"]
     assert st["lowering"] == "flash" and st["grid"] == [4 * 8 * 4, 1, 1] and st["block"] == [128, 1, 1]
     assert st["tiles"] == {"block_m": 64, "block_n": 32, "waves": 2, "parts": 4}
     assert "gr_flash32_fwd_body<64, 32, 2, true, 4>" in src32 and '#include "gr_flash_f32.h"' in src32
     assert f"__device__ float gr_ws_t_O[{4 * 4 * 256 * 64}];" in src32
+    # the second launch merges the 4 partials of each query: one thread per 8 head dims
+    assert mg["kernel"] == "t_O_merge_kernel" and mg["merge"] and mg["grid"] == [4 * 256 * 8 // 256, 1, 1]
+    assert "gr_flash32_merge_body<64, 4>" in src32
     # one workgroup per query block (every key in its waves): no workspace
     one = parse_plan(emit_module(C.p_flash_attention(B=1, H=1, N=256, d=64, bm=128, bn=64, dtype="fp32")))
-    assert one["steps"][0]["tiles"]["parts"] == 1
+    assert one["steps"][0]["tiles"]["parts"] == 1 and len(one["steps"]) == 1
     # causal fp32 stays on the generic lowering; so does a workspace past the cap
     p32c = C.p_flash_attention(B=2, H=2, N=256, d=64, bm=32, bn=32, causal=True, dtype="fp32")
     assert parse_plan(emit_module(p32c))["steps"][0]["lowering"] == "generic"
