@@ -49,6 +49,8 @@ struct gr_gemm_args {
   float alpha;
   const void* r = nullptr;        // residual R (GR_EPI_RES), laid out like C
   long long r_sb = 0, r_sm = 0;   // its batch and row strides
+  int ksplit = 1;                 // fp32 GEMM: blockIdx.z takes K part blockIdx.z of ksplit ...
+  long long c_sz = 0;             // ... and writes it at C + blockIdx.z * c_sz
 };
 
 template <int EPI>

@@ -56,10 +56,14 @@ __device__ __forceinline__ void gr_gemm_f32_body(const gr_gemm_args& a, char* ld
   const int bid = gr_xcd_remap((int)blockIdx.x, (int)gridDim.x);
   const int tm = bid / tiles_n, tn = bid % tiles_n;
   const long long z = blockIdx.y;
-  const float* A = static_cast<const float*>(a.a) + z * a.a_sb + (long long)tm * BM * a.a_sm;
+  // split K (ksplit > 1): this workgroup's part of the contraction, its
+  // partial product written to its own C slice (gr_gemm_f32_reduce_body sums them)
+  const int kpart = a.K / a.ksplit, k0 = (int)blockIdx.z * kpart;
+  const float* A = static_cast<const float*>(a.a) + z * a.a_sb + (long long)tm * BM * a.a_sm + k0;
   const float* B = static_cast<const float*>(a.b) + z * a.b_sb +
-                   (B_KMAJOR ? (long long)tn * BN * a.b_s : (long long)tn * BN);
-  float* C = static_cast<float*>(a.c) + z * a.c_sb + (long long)tm * BM * a.c_sm + (long long)tn * BN;
+                   (B_KMAJOR ? (long long)tn * BN * a.b_s + k0 : (long long)tn * BN + (long long)k0 * a.b_s);
+  float* C = static_cast<float*>(a.c) + blockIdx.z * a.c_sz + z * a.c_sb + (long long)tm * BM * a.c_sm +
+             (long long)tn * BN;
 
   gr_f32x16 acc[TN][TM];
 #pragma unroll
@@ -139,7 +143,7 @@ __device__ __forceinline__ void gr_gemm_f32_body(const gr_gemm_args& a, char* ld
     }
   };
 
-  const int nk = a.K / BK;
+  const int nk = kpart / BK;
   gload(0);
   sstore(lds);
   __syncthreads();
@@ -171,6 +175,29 @@ __device__ __forceinline__ void gr_gemm_f32_body(const gr_gemm_args& a, char* ld
         *reinterpret_cast<gr_f32x4*>(crow + col) = w;
       }
   }
+}
+
+// The second launch of a split-K GEMM: C = act(alpha * sum_s P_s) [+ R] over
+// the ksplit partial products P_s (at ws + s * ws_sz, laid out as C with
+// row stride N, batch stride M N). One thread per 4 consecutive columns of
+// one row; the grid covers batch * M * N / 4 threads in workgroups of 256.
+template <int EPI>
+__device__ __forceinline__ void gr_gemm_f32_reduce_body(const gr_gemm_args& a, const float* ws, int ksplit,
+                                                        long long ws_sz, int batch) {
+  const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long per = (long long)a.M * a.N / 4;
+  if (idx >= per * batch) return;
+  const long long z = idx / per, e4 = (idx % per) * 4;
+  const int row = (int)(e4 / a.N), col = (int)(e4 % a.N);
+  gr_f32x4 sum = (gr_f32x4)(0.f);
+  for (int s = 0; s < ksplit; ++s)
+    sum += *reinterpret_cast<const gr_f32x4*>(ws + s * ws_sz + z * a.M * (long long)a.N + e4);
+  gr_f32x4 w;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) w[e] = gr_epilogue<EPI>(a.alpha * sum[e]);
+  if constexpr ((EPI & GR_EPI_RES) != 0)
+    w += *reinterpret_cast<const gr_f32x4*>(static_cast<const float*>(a.r) + z * a.r_sb + (long long)row * a.r_sm + col);
+  *reinterpret_cast<gr_f32x4*>(static_cast<float*>(a.c) + z * a.c_sb + (long long)row * a.c_sm + col) = w;
 }
 
 template <int BM, int BN, int BK, int WGM, int WGN, bool B_KMAJOR, int EPI>

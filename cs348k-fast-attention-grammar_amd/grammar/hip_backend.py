@@ -89,6 +89,7 @@ FLASH_BM = {32: (1, 1), 64: (2, 1), 128: (4, 1), 256: (8, 1)}   # block_m -> def
 # softmax.
 FLASH_KNOBS = {"qb": (1, 2), "pipe": (0, 1)}
 FLASH_KNOB_DEFAULTS = {"qb": 1, "pipe": 0}     # what an absent knob means
+KNOB_DEFAULTS = {**FLASH_KNOB_DEFAULTS, "ksplit": 1}
 
 
 FLASH_DEFAULT_BN = {64: 128, 128: 64}    # key tile when the stage does not tile the key axis
@@ -291,10 +292,16 @@ def template_tilings(loop: ParallelLoop, program: Program) -> list:
 
 def schedule_knobs(loop: ParallelLoop, program: Program) -> dict:
     """The schedule knobs the renderer honours for this stage, each with its
-    choices and current value: {name: (choices, current)}; empty for stages
-    that do not lower to the flash kernel."""
+    choices and current value: {name: (choices, current)}: the flash kernel's
+    query blocks per wave and pipelined schedule, the fp32 GEMM's split K;
+    empty for other stages."""
     f = _match_flash(loop, program)
-    if f is None or f.get("f32"):
+    if f is None:
+        gm = _match_gemm(loop, program)
+        if gm is not None and gm.get("f32"):
+            return {"ksplit": (GEMM_KSPLIT, gm["ksplit"])}
+        return {}
+    if f.get("f32"):
         return {}
     out = {"pipe": (FLASH_KNOBS["pipe"], f["pipe"])}
     if f["D"] == 64:
@@ -398,6 +405,11 @@ void {kname}({params}) {{
 # ---------------------------------------------------------------------------
 GEMM_ACTS = {"relu": 1, "silu": 2}
 GEMM_RES = 4          # epilogue flag: + a residual tensor (GR_EPI_RES)
+# fp32 GEMM stages may split K over workgroups (schedule knob "ksplit"): the
+# partial products go to a module-scope workspace (capped at this many bytes)
+# and a second launch sums them and applies the epilogue
+GEMM_KSPLIT = (1, 2, 4, 8)
+GEMM_WS_LIMIT = 32 << 20
 GEMM_WAVES_M = {32: 1, 64: 1, 128: 2, 256: 2}
 GEMM_WAVES_N = {32: 1, 64: 1, 128: 2, 256: 2}
 
@@ -529,11 +541,17 @@ def _match_gemm(loop: ParallelLoop, program: Program):
             return None
         BK = rl.tile if rl is not None and rl.tile in (8, 16, 32) and K % rl.tile == 0 else \
             (32 if K % 32 == 0 else 16 if K % 16 == 0 else 8)
+        # split K over workgroups (schedule knob "ksplit"): a choice the shape
+        # cannot take (K / ksplit not a multiple of BK, or a workspace past the
+        # cap) keeps one part
+        ks = int((getattr(loop, "knobs", None) or {}).get("ksplit", 1))
+        if ks not in GEMM_KSPLIT or K % (ks * BK) or ks * batch * M * N * 4 > GEMM_WS_LIMIT:
+            ks = 1
         return {"a": aload.source, "b": bload.source, "c": loop.out, "M": M, "N": N, "K": K, "batch": batch,
                 "a_sb": M * K if a_batched else 0, "b_sb": K * N if b_batched else 0, "c_sb": M * N,
                 "kmajor": kmajor, "act": act, "alpha": alpha, "BM": BM, "BN": BN, "BK": BK,
                 "WGM": 2 if BM >= 64 else 1, "WGN": 2 if BN >= 64 else 1, "f32": True,
-                "res": res.source if res is not None else None}
+                "res": res.source if res is not None else None, "ksplit": ks}
     if BM not in GEMM_WAVES_M or BN not in GEMM_WAVES_N:   # ragged M, N: edge tiles store their valid part
         return None
     BK = rl.tile if rl is not None else 64
@@ -552,6 +570,51 @@ def _match_gemm(loop: ParallelLoop, program: Program):
             "res": res.source if res is not None else None}
 
 
+def _render_gemm_f32_split(loop, program, f, args, params, km) -> tuple:
+    """An fp32 GEMM stage with K split over `ksplit` workgroups: the partial
+    products go to a module-scope workspace, and a second launch sums them
+    and applies alpha, the activation and the residual (two plan steps)."""
+    ks, M, N, K, batch = f["ksplit"], f["M"], f["N"], f["K"], f["batch"]
+    kname = f"{_cname(loop.out)}_kernel"
+    rname = f"{_cname(loop.out)}_reduce_kernel"
+    ws = f"gr_ws_{_cname(loop.out)}"
+    nt = f["WGM"] * f["WGN"] * 64
+    res_line = (f"\n  a.r = {_cname(f['res'])}; a.r_sb = {f['c_sb']}LL; a.r_sm = {N};" if f.get("res") else "")
+    common = f"""  gr_gemm_args a;
+  a.a = {_cname(f['a'])}; a.b = {_cname(f['b'])}; a.c = {_cname(f['c'])};
+  a.a_sb = {f['a_sb']}LL; a.a_sm = {K};
+  a.b_sb = {f['b_sb']}LL; a.b_s = {K if f['kmajor'] else N};
+  a.c_sb = {f['c_sb']}LL; a.c_sm = {N};
+  a.M = {M}; a.N = {N}; a.K = {K};
+  a.alpha = {_flt(f['alpha'])};{res_line}"""
+    code = f"""
+// stage {loop.out}: fp32 MFMA GEMM {M}x{N}x{K} (x{batch}), tile {f['BM']}x{f['BN']}x{f['BK']}, K split over
+// {ks} workgroups; their partial products live in this module's workspace between the two launches,
+// so two runs of the module must not overlap
+__device__ float {ws}[{ks * batch * M * N}];
+extern "C" __global__ __launch_bounds__({nt})
+void {kname}({params}) {{
+  extern __shared__ __attribute__((aligned(16))) char gr_gemm_smem[];
+{common}
+  a.c = {ws}; a.c_sb = {M * N}LL; a.alpha = 1.0f; a.r = nullptr;
+  a.ksplit = {ks}; a.c_sz = {batch * M * N}LL;
+  gr_gemm_f32_body<{f['BM']}, {f['BN']}, {f['BK']}, {f['WGM']}, {f['WGN']}, {km}, 0>(a, gr_gemm_smem);
+}}
+extern "C" __global__ __launch_bounds__(256)
+void {rname}({params}) {{
+{common}
+  gr_gemm_f32_reduce_body<{f['act']}>(a, {ws}, {ks}, {batch * M * N}LL, {batch});
+}}
+"""
+    grid = (M // f["BM"]) * (N // f["BN"])
+    steps = [{"kernel": kname, "grid": [grid, batch, ks], "block": [nt, 1, 1],
+              "lds": _gemm_f32_lds(f["BM"], f["BN"], f["BK"], f["kmajor"]), "args": args, "lowering": "gemm",
+              "tiles": {"block_m": f["BM"], "block_n": f["BN"], "block_k": f["BK"], "ksplit": ks}},
+             {"kernel": rname, "grid": [_cdiv(batch * M * N // 4, 256), 1, 1], "block": [256, 1, 1], "lds": 0,
+              "args": args, "lowering": "gemm", "merge": True}]
+    return code, steps
+
+
 def _render_gemm(loop, program, f) -> tuple:
     T = CTYPE[program.dtype]
     kname = f"{_cname(loop.out)}_kernel"
@@ -560,6 +623,8 @@ def _render_gemm(loop, program, f) -> tuple:
     km = "true" if f["kmajor"] else "false"
     res_line = (f"\n  a.r = {_cname(f['res'])}; a.r_sb = {f['c_sb']}LL; a.r_sm = {f['N']};"
                 if f.get("res") else "")
+    if f.get("f32") and f.get("ksplit", 1) > 1:
+        return _render_gemm_f32_split(loop, program, f, args, params, km)
     if f.get("f32"):
         nt = f["WGM"] * f["WGN"] * 64
         code = f"""

@@ -134,10 +134,12 @@ def test_flash_schedule_knobs_reach_the_renderer_and_the_key():
     names["SCHED_O.pipe"].set(0)
     names["SCHED_O.qb"].set(1)
     assert p.body[0].knobs == {} and structural_key(p) == base_key and emit_module(p) == base_src
-    # head dim 128 offers no second query block per wave; non-flash stages offer nothing
+    # head dim 128 offers no second query block per wave
     p128 = C.p_flash_attention(B=1, H=2, N=256, d=128, bm=128, bn=64, dtype="bf16")
     assert [q.name for q in O.parameter_vector(p128) if q.name.startswith("SCHED_")] == ["SCHED_O.pipe"]
-    assert not [q for q in O.parameter_vector(C.p_attention_atomic()) if q.name.startswith("SCHED_")]
+    # the atomic fp32 program offers no flash knobs; its fp32 GEMM stages (S, O) offer split K
+    sched = [q.name for q in O.parameter_vector(C.p_attention_atomic()) if q.name.startswith("SCHED_")]
+    assert sched == ["SCHED_S.ksplit", "SCHED_O.ksplit"], sched
 
 
 def test_fp16_flash_with_large_scale_skips_the_q_prescale():
@@ -182,3 +184,31 @@ def test_residual_add_lowers_to_the_gemm_epilogue():
         st = [s for s in parse_plan(src)["steps"] if s["kernel"] == "t_r_kernel"][0]
         assert st["lowering"] == "gemm" and "t_X" in src.split("void t_r_kernel(")[1].split(")")[0]
         assert "a.r = t_X; a.r_sb = 131072LL; a.r_sm = 512;" in src and body in src, dt
+
+
+def test_fp32_gemm_split_k_knob():
+    """fp32 GEMM stages offer the schedule knob ksplit: the K loop split over
+    workgroups (grid z), the partials in a module-scope workspace, and a
+    second launch that sums them and applies alpha, the activation and the
+    residual. A split that does not divide K into whole k tiles keeps one part."""
+    import run_mlp_search as RM
+    from grammar import rewrites as R
+    from grammar.hip_backend import schedule_knobs
+    from grammar.kernel_ast import structural_key
+    p = RM.build_mlp_ln(256, 512, 1024, tile=64)
+    p = R.merge(p, p.body[2], p.body[3])
+    r = p.body[2]
+    assert r.out == "r" and schedule_knobs(r, p) == {"ksplit": ((1, 2, 4, 8), 1)}
+    key0 = structural_key(p)
+    r.knobs["ksplit"] = 4
+    assert structural_key(p) != key0
+    src = emit_module(p)
+    steps = [s for s in parse_plan(src)["steps"] if s["kernel"].startswith("t_r_")]
+    assert [s["kernel"] for s in steps] == ["t_r_kernel", "t_r_reduce_kernel"]
+    assert steps[0]["grid"] == [(256 // 64) * (512 // 64), 1, 4] and steps[0]["tiles"]["ksplit"] == 4
+    assert steps[1]["merge"] and steps[1]["grid"] == [256 * 512 // 4 // 256, 1, 1]
+    assert "__device__ float gr_ws_t_r[524288];" in src and "gr_gemm_f32_reduce_body<4>(a, gr_ws_t_r, 4" in src
+    r.knobs["ksplit"] = 8                       # 1024 / 8 = 128: whole 32-deep k tiles
+    assert [s for s in parse_plan(emit_module(p))["steps"] if s["kernel"] == "t_r_kernel"][0]["tiles"]["ksplit"] == 8
+    p16 = RM.build_mlp_ln(256, 512, 1024, tile=64, dtype="fp16")
+    assert schedule_knobs(p16.body[2], p16) == {}   # fp16 GEMMs take no split

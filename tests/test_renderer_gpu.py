@@ -322,6 +322,42 @@ def test_residual_add_fuses_into_the_gemm(dt):
         assert np.isfinite(got).all() and err <= tol * max(1.0, float(np.max(np.abs(want[name]))))
 
 
+@pytest.mark.parametrize("ks_a,ks_r", [(2, 4), (8, 8), (4, 1)])
+def test_fp32_split_k_gemm_stages(ks_a, ks_r):
+    """fp32 GEMM stages with K split over workgroups (schedule knob ksplit):
+    the ReLU stage and the residual stage of the merged LN block against the
+    tile interpreter; two runs of the bound plan give the same bits."""
+    _cuda()
+    import run_mlp_search as RM
+    from grammar import rewrites as R
+    from grammar.hip_module import load_module
+    p = RM.build_mlp_ln(256, 256, 512, tile=64)
+    p = R.merge(p, p.body[2], p.body[3])
+    p = R.merge(p, p.body[0], p.body[1])
+    p.body[0].knobs["ksplit"] = ks_a
+    p.body[1].knobs["ksplit"] = ks_r
+    mod = load_module(emit_module(p))
+    tiles = [s.get("tiles", {}).get("ksplit", 1) for s in mod.plan["steps"] if not s.get("merge")]
+    assert tiles[:2] == [ks_a, ks_r], tiles
+    ins = {k: v.cpu().numpy() for k, v in RM.mlp_inputs(256, 256, 512, "fp32", seed=4).items()}
+    args = [torch.from_numpy(ins[n]).to(_cuda()) for n in mod.inputs]
+    tensors = {n: t for n, t in zip(mod.inputs, args)}
+    tensors.update(mod.allocate(args[0].device))
+    plan = mod.bind(tensors)
+    plan.run()
+    torch.cuda.synchronize()
+    first = {n: tensors[n].clone() for n in ("a", "r", "out")}
+    plan.run()
+    torch.cuda.synchronize()
+    want = run_program(p, ins)
+    for name in ("a", "r", "out"):
+        got = tensors[name].cpu().numpy()
+        err = float(np.max(np.abs(got - want[name])))
+        print(f"[split-k] ksplit {ks_a}/{ks_r} {name}: max|d| {err:.2e}", flush=True)
+        assert err <= 1e-3 * max(1.0, float(np.max(np.abs(want[name]))))
+        assert torch.equal(tensors[name], first[name])
+
+
 @pytest.mark.parametrize("dt,causal,merges", [("fp16", False, 0), ("bf16", True, 0), ("fp16", False, 3)])
 def test_row_lowered_softmax_stages(dt, causal, merges):
     """The softmax stages of the atomic attention program (scale, causal
