@@ -1,0 +1,117 @@
+"""The reference's own descent-found programs on the MI355X.
+
+The reference commits, per ablation run, the program its descent held at each
+improvement (runs/attn_*/log.jsonl `best_key`, re-benched on an L4 into
+runs/attn_*/results/it*.json; run_attention_search.py:117-166,
+bench.py:89-140). Their structural keys are kept as data in
+tests/golden/reference_runs.json (42 programs, all of the reference's
+workload: one head, N = 512, d = 64, fp32). This script rebuilds each
+feasible one from its key, renders it with this grammar's HIP backend
+unchanged (the reference's own stages and tile sizes: no rewrite, no
+re-tiling), checks its output against the float64 closed form and times it:
+
+    python run_reference_programs.py [--programs PATH] [--out runs/reference_programs.json]
+
+The output lists per program the run, iteration, stages, the lowering each
+stage got, the max-abs error and the time (hipEvents around back-to-back runs
+after a clock ramp), beside the reference's own L4 figure where the reference
+published one (results/attn-*.json: its final best programs)."""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+DEFAULT_PROGRAMS = os.path.join(HERE, "..", "tests", "golden", "reference_runs.json")
+
+# The reference's published L4 times of its final best programs
+# (results/attn-{full,norev,nojump,nolocal}.json, mean ms of 200 runs).
+REFERENCE_L4_MS = {("attn_full", 24): 0.10630, ("attn_norev", 36): 0.10441,
+                   ("attn_nojump", 28): 0.10687, ("attn_nolocal", 20): 0.10293}
+
+
+def closed_form(q, kt, v):
+    """softmax(Q KT / sqrt(d)) V in float64 (run_attention_search.py:176-180)."""
+    import numpy as np
+    s = (q.astype(np.float64) @ kt.astype(np.float64)) / np.sqrt(q.shape[-1])
+    e = np.exp(s - s.max(-1, keepdims=True))
+    return (e / e.sum(-1, keepdims=True)) @ v.astype(np.float64)
+
+
+def measure(records: list, steps: int, ramp_ms: float, seed: int) -> list:
+    import numpy as np
+    import torch
+    from concurrent.futures import ThreadPoolExecutor
+    from grammar import runtime as rt
+    from grammar.hip_module import HipModule, compile_cached
+    from grammar.kernel_ast import emit_module, program_from_key
+
+    srcs = [emit_module(program_from_key(r["key"])) for r in records]
+    with ThreadPoolExecutor(max_workers=8) as pool:          # hiprtc compiles release the GIL
+        codes = list(pool.map(lambda s: compile_cached(s)[0], srcs))
+    out = []
+    for r, src, code in zip(records, srcs, codes):
+        mod = HipModule(src, code)
+        g = torch.Generator("cpu").manual_seed(seed)
+        host = {n: torch.randn(tuple(s), generator=g) for n, s in mod.KERNEL_META["inputs"]}
+        tensors = {n: t.cuda() for n, t in host.items()}
+        tensors.update(mod.allocate("cuda"))
+        plan = mod.bind(tensors)
+        plan.run()
+        torch.cuda.synchronize()
+        got = tensors[mod.plan["outputs"][0]].double().cpu().numpy()
+        want = closed_form(host["Q"].numpy(), host["KT"].numpy(), host["V"].numpy())
+        err = float(np.max(np.abs(got - want)))
+        t0 = time.time()
+        while (time.time() - t0) * 1e3 < ramp_ms:
+            plan.time(0, 50, rt.GR_TIME_BATCH)
+        ms = plan.time(0, steps, rt.GR_TIME_BATCH)
+        flops = mod.KERNEL_META["flops"]
+        rec = {"run": r["run"], "iter": r["iter"], "stages": [s[0] for s in r["stages"]],
+               "tiles": [s[1] for s in r["stages"]],
+               "lowering": [[st["kernel"], st["lowering"]] for st in mod.plan["steps"]],
+               "launches": len(mod.plan["steps"]), "max_abs_err": err, "ms": ms,
+               "tflops": flops / (ms * 1e-3) / 1e12, "flops": flops}
+        l4 = REFERENCE_L4_MS.get((r["run"], r["iter"]))
+        if l4 is not None:
+            rec["reference_l4_ms"] = l4
+        out.append(rec)
+        print(f"{r['run']:>14s} it{r['iter']:<3d} {len(r['stages'])} stages  "
+              f"{ms * 1e3:8.1f} us  err {err:.1e}" + (f"   (L4: {l4 * 1e3:.1f} us)" if l4 else ""), flush=True)
+        del plan, tensors, mod
+    return out
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--programs", default=DEFAULT_PROGRAMS)
+    ap.add_argument("--out", default=os.path.join(HERE, "runs", "reference_programs.json"))
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--ramp-ms", type=float, default=50.0, dest="ramp_ms")
+    ap.add_argument("--seed", type=int, default=0)
+    args = ap.parse_args(argv)
+    import torch
+    if not torch.cuda.is_available():
+        print("run_reference_programs.py needs a GPU", file=sys.stderr)
+        return 2
+    with open(args.programs) as f:
+        records = [r for r in json.load(f)["records"] if r["loss_kind"] == "feasible"]
+    out = measure(records, args.steps, args.ramp_ms, args.seed)
+    doc = ("The reference's own descent-found programs (tests/golden/reference_runs.json, from its "
+           "runs/*/log.jsonl), rendered unchanged by this grammar's HIP backend and timed on one MI355X: "
+           "python run_reference_programs.py")
+    with open(args.out, "w") as f:
+        json.dump({"_doc": doc, "device": torch.cuda.get_device_name(0), "steps": args.steps,
+                   "records": out}, f, indent=1)
+    worst = max(r["max_abs_err"] for r in out)
+    print(f"{len(out)} programs, worst max-abs error {worst:.1e}; wrote {args.out}")
+    return 0 if worst <= 1e-3 else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())
