@@ -350,6 +350,8 @@ def run_descent(cfg, seconds: float, seed: int):
             wall = time.time() - t0
             st = ev.stats()
             best_loss = ev(best)
+            # the search's best few, timed again side by side with warm clocks
+            best, finalists = ev.refine(k=6)
             ev.close()
         finally:
             if old is None:
@@ -365,6 +367,10 @@ def run_descent(cfg, seconds: float, seed: int):
                            "the code-object cache starts empty"),
             "best_loss_ms": round(best_loss, 6), "start": "naive 8-stage program, full-extent tiles",
             "stages": [[l.out, list(l.tile_shape)] for l in best.body],
+            "finalists": [{"stages": r["stages"], "tiles": r["tiles"], "search_ms": round(r["search_ms"], 6),
+                           "refined_ms": round(r["refined_ms"], 6)} for r in finalists],
+            "finalists_note": ("the search's best distinct programs re-timed side by side (median of 3 rounds "
+                               "of 200 back-to-back runs after a 50 ms clock ramp); the fastest is benchmarked"),
             "best_so_far": best_so_far(ev.timeline, cfg.flops)}
     return best, info
 

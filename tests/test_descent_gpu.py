@@ -130,6 +130,20 @@ def test_live_descent_finds_a_kernel_that_passes_the_oracle(tmp_path, monkeypatc
         oref = O.attention(ins["Q"].float().numpy(), ins["KT"].float().numpy(), ins["V"].float().numpy(),
                            k_transposed=True)
         _check(out, oref, "live descent best")
+        # the finalists re-timed side by side: distinct scored programs, fastest first, and
+        # the one returned is a scored, checked program that also passes the oracle
+        from grammar.kernel_ast import structural_key
+        fast, recs = ev.refine(k=3, rounds=2, iters=20, ramp_ms=5.0)
+        print(f"[refine] {[(r['stages'], r['search_ms'], r['refined_ms']) for r in recs]}", flush=True)
+        assert 1 <= len(recs) <= 3
+        assert [r["refined_ms"] for r in recs] == sorted(r["refined_ms"] for r in recs)
+        assert all(r["refined_ms"] > 0 for r in recs)
+        assert structural_key(fast) in ev._cache and ev(fast) < 1e9
+        assert len({emit_module(r["program"]) for r in recs}) == len(recs)
+        mod = HipModule(emit_module(fast))
+        out = mod.fn(*[ins[n].to(dev) for n in mod.inputs])
+        torch.cuda.synchronize()
+        _check(out, oref, "refined best")
     finally:
         ev.close()
 

@@ -169,3 +169,11 @@ def test_stage1_reaches_template_tilings_in_one_move():
     finally:
         O._template_snaps = keep
     assert [s["lowering"] for s in parse_plan(emit_module(out))["steps"]][:2] == ["generic", "generic"]
+
+
+def test_refine_needs_timed_scores():
+    """Re-timing the finalists is a GPU step: proxy scores have nothing to re-time."""
+    ev = _ev()
+    ev(C.p_attention_atomic())
+    with pytest.raises(RuntimeError, match="proxy"):
+        ev.refine(k=3)
