@@ -15,7 +15,9 @@ re-tiling), checks its output against the float64 closed form and times it:
 The output lists per program the run, iteration, stages, the lowering each
 stage got, the max-abs error and the time (hipEvents around back-to-back runs
 after a clock ramp), beside the reference's own L4 figure where the reference
-published one (results/attn-*.json: its final best programs)."""
+published one (results/attn-*.json: its final best programs), and the
+reference's GPU baselines at the same workload on this GPU: the staged naive
+torch path and torch's SDPA (results/naive-pytorch.json, flash2-sota.json)."""
 from __future__ import annotations
 
 import argparse
@@ -87,6 +89,54 @@ def measure(records: list, steps: int, ramp_ms: float, seed: int) -> list:
     return out
 
 
+def naive_staged(kt, q, v):
+    """The reference's staged naive baseline (pytorch-naive.py:23-65), every
+    intermediate materialised, with its two slips corrected: the row max is a
+    max (the reference sums), and the row vectors keep their [N, 1] shape so
+    they broadcast along the key axis."""
+    import torch
+    s = q @ kt
+    s = s * (q.shape[-1] ** -0.5)
+    mx = torch.amax(s, dim=1, keepdim=True)
+    e = torch.exp(s - mx)
+    sm = torch.sum(e, dim=1, keepdim=True)
+    return (e / sm) @ v
+
+
+def baselines(steps: int, ramp_ms: float, seed: int) -> dict:
+    """The reference's own GPU baselines at its workload, on this GPU:
+    the staged naive torch path (results/naive-pytorch.json) and torch's
+    scaled_dot_product_attention (flash-attn2-sota.py:41-62,
+    results/flash2-sota.json), fp32, one head, N = 512, d = 64."""
+    import torch
+    import torch.nn.functional as F
+    g = torch.Generator("cpu").manual_seed(seed)
+    q, kt, v = (torch.randn(512, 64, generator=g).cuda(), torch.randn(64, 512, generator=g).cuda(),
+                torch.randn(512, 64, generator=g).cuda())
+    q4, k4, v4 = q.view(1, 1, 512, 64), kt.t().contiguous().view(1, 1, 512, 64), v.view(1, 1, 512, 64)
+    want = closed_form(q.double().cpu().numpy(), kt.double().cpu().numpy(), v.double().cpu().numpy())
+    out = {}
+    for name, step in (("naive_torch", lambda: naive_staged(kt, q, v)),
+                       ("torch_sdpa", lambda: F.scaled_dot_product_attention(q4, k4, v4))):
+        got = step().reshape(512, 64).double().cpu().numpy()
+        err = float(abs(got - want).max())
+        t0 = time.time()
+        while (time.time() - t0) * 1e3 < ramp_ms:
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        e1.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        out[name] = {"ms": ms, "max_abs_err": err, "tflops": 68681728 / (ms * 1e-3) / 1e12}
+        print(f"{name:>14s}: {ms * 1e3:8.1f} us  err {err:.1e}", flush=True)
+    out["torch_sdpa"]["backend_note"] = "torch.nn.functional.scaled_dot_product_attention, fp32 inputs"
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--programs", default=DEFAULT_PROGRAMS)
@@ -102,12 +152,15 @@ def main(argv=None) -> int:
     with open(args.programs) as f:
         records = [r for r in json.load(f)["records"] if r["loss_kind"] == "feasible"]
     out = measure(records, args.steps, args.ramp_ms, args.seed)
+    base = baselines(args.steps, args.ramp_ms, args.seed)
     doc = ("The reference's own descent-found programs (tests/golden/reference_runs.json, from its "
            "runs/*/log.jsonl), rendered unchanged by this grammar's HIP backend and timed on one MI355X: "
            "python run_reference_programs.py")
     with open(args.out, "w") as f:
         json.dump({"_doc": doc, "device": torch.cuda.get_device_name(0), "steps": args.steps,
-                   "records": out}, f, indent=1)
+                   "records": out, "baselines": base,
+                   "reference_l4_baselines_ms": {"naive_torch": 0.21396, "torch_sdpa": 0.06731,
+                                                 "manual_cutile": 2.39624}}, f, indent=1)
     worst = max(r["max_abs_err"] for r in out)
     print(f"{len(out)} programs, worst max-abs error {worst:.1e}; wrote {args.out}")
     return 0 if worst <= 1e-3 else 1
