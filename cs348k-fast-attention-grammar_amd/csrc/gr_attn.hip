@@ -6,6 +6,7 @@
 #include <mutex>
 
 #include "gr_flash_decode.h"
+#include "gr_flash_f32.h"
 #include "gr_host.h"
 #include "grammar_rt.h"
 
@@ -227,6 +228,42 @@ __global__ void gr_selftest_mfma32_kernel(const _Float16* A, const _Float16* B, 
 
 namespace {
 
+// fp32 (the reference's own dtype) on the fp32 matrix cores: a workgroup owns
+// 32 queries and splits all N keys over its NW waves (merged through LDS), so
+// one launch suffices and no workspace is needed.
+template <int D, int NW, bool KT>
+__global__ __launch_bounds__(NW * 64) void gr_flash32_kernel(gr_attn_args a, int nkb) {
+  extern __shared__ __attribute__((aligned(16))) char gr_lds[];
+  gr_flash32_fwd_body<D, 32, NW, KT, 1>(a, gr_lds, nullptr, nullptr, nkb);
+}
+
+template <int D, bool KT>
+int launch_flash32(const gr_attn_args& a, hipStream_t st) {
+  const int nw = a.N % 128 == 0 ? 4 : (a.N % 64 == 0 ? 2 : 1);
+  const int nkb = a.N / (32 * nw);
+  const long long nblk = (long long)a.B * a.H * (a.N / 32);
+  if (nblk <= 0 || nblk > 0x7fffffffLL) return gr::fail(GR_E_ARG, "gr_attn_fwd: grid size %lld out of range", nblk);
+  if (nw == 4)
+    hipLaunchKernelGGL((gr_flash32_kernel<D, 4, KT>), dim3((unsigned)nblk), dim3(256), (gr_flash32_lds<D, 4>::BYTES),
+                       st, a, nkb);
+  else if (nw == 2)
+    hipLaunchKernelGGL((gr_flash32_kernel<D, 2, KT>), dim3((unsigned)nblk), dim3(128), (gr_flash32_lds<D, 2>::BYTES),
+                       st, a, nkb);
+  else
+    hipLaunchKernelGGL((gr_flash32_kernel<D, 1, KT>), dim3((unsigned)nblk), dim3(64), (gr_flash32_lds<D, 1>::BYTES),
+                       st, a, nkb);
+  return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_fwd fp32 launch");
+}
+
+int attn_fwd_f32(const gr_attn_args& a, int D, bool causal, bool k_transposed, bool train, hipStream_t st) {
+  if (causal) return gr::fail(GR_E_ARG, "gr_attn_fwd: fp32 is non-causal only (the reference's fp32 workload)");
+  if (train) return gr::fail(GR_E_ARG, "gr_attn_fwd_train: fp32 has no training path (GR_F16 or GR_BF16)");
+  if (a.N % 32) return gr::fail(GR_E_ARG, "gr_attn_fwd: fp32 needs N a multiple of 32 (got %d)", a.N);
+  if (D == 64) return k_transposed ? launch_flash32<64, true>(a, st) : launch_flash32<64, false>(a, st);
+  if (D == 128) return k_transposed ? launch_flash32<128, true>(a, st) : launch_flash32<128, false>(a, st);
+  return gr::fail(GR_E_ARG, "gr_attn_fwd: head dim %d unsupported (64 or 128)", D);
+}
+
 int attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int dtype, int B, int H, int N, int D,
              const long long* qs, const long long* ks, const long long* vs, const long long* os, int k_transposed,
              int causal, float scale, int block_m, int block_n, void* stream) {
@@ -265,7 +302,8 @@ int attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, i
   hipStream_t st = (hipStream_t)stream;
   if (dtype == GR_F16) return dispatch_shape<_Float16>(a, D, causal != 0, k_transposed != 0, block_m, block_n, st);
   if (dtype == GR_BF16) return dispatch_shape<__bf16>(a, D, causal != 0, k_transposed != 0, block_m, block_n, st);
-  return gr::fail(GR_E_ARG, "gr_attn_fwd: dtype %d unsupported (GR_F16 or GR_BF16)", dtype);
+  if (dtype == GR_F32) return attn_fwd_f32(a, D, causal != 0, k_transposed != 0, lse != nullptr, st);
+  return gr::fail(GR_E_ARG, "gr_attn_fwd: dtype %d unsupported (GR_F16, GR_BF16 or GR_F32)", dtype);
 }
 
 }  // namespace

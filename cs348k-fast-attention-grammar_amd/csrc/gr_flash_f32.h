@@ -38,9 +38,12 @@ struct gr_flash32_lds {
   static constexpr int BYTES = (O_FLOATS + NW * 32 * 2) * 4;
 };
 
+// nkb: 32-key blocks per wave when the chunk length is only known at run time
+// (the library launch, PARTS = 1: nkb = N / (32 NW)); 0 takes BN / 32.
 template <int D, int BN, int NW, bool KT_LAYOUT, int PARTS>
-__device__ __forceinline__ void gr_flash32_fwd_body(const gr_attn_args& a, char* lds, float* ws_o, float* ws_ml) {
-  constexpr int KB = BN / 32;      // 32-key blocks per wave
+__device__ __forceinline__ void gr_flash32_fwd_body(const gr_attn_args& a, char* lds, float* ws_o, float* ws_ml,
+                                                    int nkb = 0) {
+  const int KB = nkb > 0 ? nkb : BN / 32;   // 32-key blocks per wave
   constexpr int DB = D / 32;       // 32-wide head-dim blocks of O^T
   constexpr int DG = D / 8;        // groups of 8 d (4 MFMAs of 2)
   constexpr int SL = D / NW;       // head dims each wave merges
@@ -59,7 +62,7 @@ __device__ __forceinline__ void gr_flash32_fwd_body(const gr_attn_args& a, char*
   const float* Kp = (const float*)a.k + b * a.k_sb + h * a.k_sh;
   const float* Vp = (const float*)a.v + b * a.v_sb + h * a.v_sh;
   float* Op = (float*)a.o + b * a.o_sb + h * a.o_sh;
-  const int q0 = qblk * 32, k0 = (part * NW + wave) * BN;
+  const int q0 = qblk * 32, k0 = (part * NW + wave) * 32 * KB;
   const float c = a.scale_log2;
 
   gr_f32x4 qf[DG];

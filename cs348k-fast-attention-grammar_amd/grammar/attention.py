@@ -1,7 +1,8 @@
 """Python face of the hand-written CDNA4 attention forward (gr_attn_fwd).
 
 `flash_attention_fwd(q, k, v)` computes softmax(scale * q k^T [causal]) v for
-[B, H, N, D] fp16/bf16 tensors on the GPU -- the same math as the reference's
+[B, H, N, D] fp16/bf16 tensors (or fp32 ones, non-causal, on the fp32 matrix
+cores) on the GPU -- the same math as the reference's
 attention module contract `fn(KT, Q, V)` (pytorch-naive.py:23-65,
 run_attention_search.py:169-181) and its SDPA reference point
 (flash-attn2-sota.py:41-62), batched over B and H.

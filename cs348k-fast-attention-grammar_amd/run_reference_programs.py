@@ -105,9 +105,11 @@ def naive_staged(kt, q, v):
 
 def baselines(steps: int, ramp_ms: float, seed: int) -> dict:
     """The reference's own GPU baselines at its workload, on this GPU:
-    the staged naive torch path (results/naive-pytorch.json) and torch's
+    the staged naive torch path (results/naive-pytorch.json), torch's
     scaled_dot_product_attention (flash-attn2-sota.py:41-62,
-    results/flash2-sota.json), fp32, one head, N = 512, d = 64."""
+    results/flash2-sota.json) and, for its hand-written kernel
+    (manual-kernal-source.py, results/manual.json), this library's
+    hand-written fp32 attention; fp32, one head, N = 512, d = 64."""
     import torch
     import torch.nn.functional as F
     g = torch.Generator("cpu").manual_seed(seed)
@@ -116,8 +118,11 @@ def baselines(steps: int, ramp_ms: float, seed: int) -> dict:
     q4, k4, v4 = q.view(1, 1, 512, 64), kt.t().contiguous().view(1, 1, 512, 64), v.view(1, 1, 512, 64)
     want = closed_form(q.double().cpu().numpy(), kt.double().cpu().numpy(), v.double().cpu().numpy())
     out = {}
+    from grammar.attention import bind_flash_attention
+    hand, _ = bind_flash_attention(q4, kt.view(1, 1, 64, 512), v4, k_transposed=True)
     for name, step in (("naive_torch", lambda: naive_staged(kt, q, v)),
-                       ("torch_sdpa", lambda: F.scaled_dot_product_attention(q4, k4, v4))):
+                       ("torch_sdpa", lambda: F.scaled_dot_product_attention(q4, k4, v4)),
+                       ("hand_written_fp32", hand)):
         got = step().reshape(512, 64).double().cpu().numpy()
         err = float(abs(got - want).max())
         t0 = time.time()
@@ -134,6 +139,8 @@ def baselines(steps: int, ramp_ms: float, seed: int) -> dict:
         out[name] = {"ms": ms, "max_abs_err": err, "tflops": 68681728 / (ms * 1e-3) / 1e12}
         print(f"{name:>14s}: {ms * 1e3:8.1f} us  err {err:.1e}", flush=True)
     out["torch_sdpa"]["backend_note"] = "torch.nn.functional.scaled_dot_product_attention, fp32 inputs"
+    out["hand_written_fp32"]["note"] = ("gr_attn_fwd with GR_F32 (one launch: 16 workgroups of 32 queries, "
+                                        "four waves splitting the keys), the counterpart of manual-kernal-source.py")
     return out
 
 

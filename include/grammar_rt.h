@@ -105,7 +105,10 @@ int gr_plan_time(gr_plan* p, void* stream, int warmup, int iters, int mode, floa
  *  rounds Q * scale * log2(e) to fp16 once (the scores then need no per-score
  *  scaling); that cannot overflow when scale * log2(e) <= 1 (as for the
  *  default 1/sqrt(D) with D >= 3), and a larger fp16 scale is refused with
- *  GR_E_ARG (bf16 takes any scale).
+ *  GR_E_ARG (bf16 takes any scale). GR_F32 (the reference's own dtype, fp32
+ *  throughout on the fp32 matrix cores): non-causal only, N a multiple of 32,
+ *  block_m and block_n ignored (a workgroup owns 32 queries and splits all N
+ *  keys over its waves); not for gr_attn_fwd_train.
  *  Q, V, O: [B, H, N, D] with strides {batch, head, seq} in elements
  *  (unit stride along D). K: [B, H, N, D] if k_transposed == 0, else KT
  *  [B, H, D, N] whose k_strides = {batch, head, d} (unit stride along N).

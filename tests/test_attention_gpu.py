@@ -155,6 +155,47 @@ def test_c3_causal_bf16_full_size():
         _check(o[b, h], ref, f"C3 head ({b},{h})")
 
 
+F32 = [
+    # B, H, N, D, k_transposed: waves per workgroup 4 (N % 128 == 0), 2 (N % 64), 1
+    (1, 1, 512, 64, True),                   # the reference's own workload
+    (2, 3, 256, 128, False),
+    (1, 2, 192, 64, True),
+    (1, 1, 96, 128, False),
+    (2, 1, 32, 64, False),
+]
+
+
+@pytest.mark.parametrize("case", F32, ids=lambda c: "-".join(map(str, c)))
+def test_attention_fp32_parity(case):
+    """fp32 throughout (the reference's dtype) against the float64 oracle at
+    the reference's fp32 bar, rtol = atol = 1e-3 (test_renderer.py:222-223)."""
+    dev = _cuda()
+    B, H, N, D, kt = case
+    g = torch.Generator("cpu").manual_seed(5)
+    q = torch.randn(B, H, N, D, generator=g)
+    k = torch.randn(B, H, D, N, generator=g) if kt else torch.randn(B, H, N, D, generator=g)
+    v = torch.randn(B, H, N, D, generator=g)
+    ref = O.attention(q.numpy(), k.numpy(), v.numpy(), k_transposed=kt, dtype=np.float64)
+    o = _run(q.to(dev), k.to(dev), v.to(dev), k_transposed=kt)
+    got = o.double().cpu().numpy()
+    print(f"[parity] fp32 {case}: max-abs {np.abs(got - ref).max():.2e}", flush=True)
+    assert np.allclose(got, ref, rtol=1e-3, atol=1e-3)
+
+
+def test_attention_fp32_rejects_what_it_does_not_cover():
+    dev = _cuda()
+    from grammar import runtime as rt
+    from grammar.attention import flash_attention_fwd_train
+    q = torch.zeros(1, 1, 128, 64, dtype=torch.float32, device=dev)
+    with pytest.raises(rt.GrError, match="non-causal"):
+        _run(q, q, q, causal=True)
+    with pytest.raises(rt.GrError, match="training"):
+        flash_attention_fwd_train(q, q, q)
+    q = torch.zeros(1, 1, 100, 64, dtype=torch.float32, device=dev)
+    with pytest.raises(rt.GrError, match="multiple of 32"):
+        _run(q, q, q)
+
+
 def test_rejects_bad_shapes():
     dev = _cuda()
     from grammar import runtime as rt
