@@ -106,12 +106,19 @@ CLOCK_RAMP_MS = 50.0   # the GPU clocks ramp up over the first tens of milliseco
 _ramps: list = []       # (label-free) ramp steps of every timed() call, for the JSON line
 
 
+HOLD_CYCLES = 200_000   # ~0.1 ms of device spin ahead of the timed steps (see timed())
+
+
 def timed(step, steps: int, warmup: int, ramp_ms: float = CLOCK_RAMP_MS) -> float:
     """ms per step, the same way for every leg: `warmup` untimed calls, then
     further untimed calls until the GPU has been kept busy for `ramp_ms` of
     wall time (its clocks ramp up over the first tens of milliseconds of
     load; the count of these extra calls is recorded), then `steps` calls
-    between two events on the current stream, synchronized on both sides."""
+    between two events on the current stream, synchronized on both sides.
+    After the synchronize a short device spin (torch.cuda._sleep, untimed:
+    it precedes the first event) holds the stream while the host enqueues
+    the timed steps, so that the first step's host launch latency -- about
+    one step at C2, 5 % of a 20-step window -- is not counted as GPU time."""
     import torch
     for _ in range(warmup):
         step()
@@ -128,6 +135,9 @@ def timed(step, steps: int, warmup: int, ramp_ms: float = CLOCK_RAMP_MS) -> floa
     stream = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
+    hold = getattr(torch.cuda, "_sleep", None)
+    if hold is not None:
+        hold(HOLD_CYCLES)
     e0.record(stream)
     for _ in range(steps):
         step()
@@ -604,6 +614,7 @@ def main() -> int:
         "warmup": args.warmup,
         "clock_ramp_ms": CLOCK_RAMP_MS,
         "clock_ramp_steps": ramp_steps,
+        "launch_hold_cycles": HOLD_CYCLES,
         "ms_per_step": round(ms, 6),
         "higher_is_better": True,
         "scaling": "weak",
