@@ -93,6 +93,9 @@ void gr_plan_free(gr_plan* p);
  *      bench.py:49-74) ------------------------------------------------------ */
 #define GR_TIME_BATCH 0   /* one event pair around `iters` back-to-back runs; mean ms */
 #define GR_TIME_MIN 1     /* one event pair per run; minimum ms over `iters` */
+/* Each event pair is preceded by a short bounded device spin (about 28 us)
+ * that holds the stream while the host enqueues the timed launches, so the
+ * time is the GPU's, without the host's launch latency. */
 int gr_plan_time(gr_plan* p, void* stream, int warmup, int iters, int mode, float* ms_out);
 
 /* ---- hand-written CDNA4 baselines -------------------------------------- */
