@@ -44,10 +44,13 @@ def test_validate_rejects_inner_to_outer_flow():
 
 def test_cache_dedup():
     cache = RenderCache()
-    cache._src[structural_key(C.p_matmul_reduction())] = "src"      # pre-seeded: emission is backend work
     k1 = structural_key(C.p_matmul_reduction())
     k2 = structural_key(C.p_matmul_reduction())
     assert k1 == k2
+    src, hit = cache.module(C.p_matmul_reduction())          # two separately built, equal programs
+    again, hit2 = cache.module(C.p_matmul_reduction())
+    assert (hit, hit2) == (False, True) and again == src
+    assert cache.result(C.p_matmul_reduction()) is None
     cache.record(C.p_matmul_reduction(), 1.23)
     assert cache.result(C.p_matmul_reduction()) == 1.23
 
