@@ -340,6 +340,34 @@ def shard_shapes(steps: int, seed: int) -> dict:
     return out
 
 
+def fp32_attention(steps: int, seed: int) -> dict:
+    """The fp32 configs through gr_attn_fwd's fp32 path: C1 as BASELINE.json
+    gives it (B1 H4 N256 d64) and the reference's own workload (one head,
+    N = 512, d = 64, K given transposed), each checked against torch fp32."""
+    import torch
+    from grammar.attention import bind_flash_attention
+    from grammar.workloads import C1, attention_inputs
+    dev = torch.device("cuda:0")
+    out = {}
+    g = torch.Generator("cpu").manual_seed(seed)
+    ref_q, ref_kt, ref_v = (torch.randn(1, 1, 512, 64, generator=g), torch.randn(1, 1, 64, 512, generator=g),
+                            torch.randn(1, 1, 512, 64, generator=g))
+    cases = (("C1", attention_inputs(C1, seed=seed), False, C1.flops),
+             ("reference_workload", (ref_q, ref_kt, ref_v), True, 4 * 512 * 512 * 64))
+    for name, (q, k, v), kt, flops in cases:
+        q, k, v = q.to(dev), k.to(dev), v.to(dev)
+        launch, o = bind_flash_attention(q, k, v, k_transposed=kt)
+        launch()
+        kk = k if kt else k.transpose(-1, -2)
+        want = torch.softmax(torch.matmul(q, kk.contiguous()) / math.sqrt(q.shape[-1]), dim=-1) @ v
+        err = float((o - want).abs().max())
+        ms = timed(launch, steps, 3)
+        out[name] = {"shape": list(q.shape), "k_transposed": kt, "ms_per_step": round(ms, 6),
+                     "tflops": round(flops / (ms * 1e-3) / 1e12, 3), "max_abs_err": err, "check_pass": err <= 1e-3}
+        log(f"[bench] fp32 {name}: {ms * 1e3:.2f} us/step  err {err:.1e}")
+    return out
+
+
 def run_descent(cfg, seconds: float, seed: int):
     """The rewrite descent from the naive program for at most `seconds`
     (500 iterations at most, C5), with a fresh, empty code-object cache so
@@ -594,6 +622,7 @@ def main() -> int:
     sdpa = None if args.no_side else sdpa_reference(args.steps, args.seed)
     training = None if args.no_side else attention_training(args.steps, args.seed)
     shards = None if args.no_side else shard_shapes(args.steps, args.seed)
+    fp32 = None if args.no_side else fp32_attention(args.steps, args.seed)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -635,6 +664,7 @@ def main() -> int:
         "mlp_c4": mlp,
         "descent_programs": side,
         "torch_sdpa": sdpa,
+        "fp32_attention": fp32,
         "training": training,
         "one_gpu_share": shards,
         "cpu_baseline": cpu,

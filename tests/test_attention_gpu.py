@@ -99,12 +99,25 @@ def test_attention_small_parity(case):
 
 
 def test_c1_shape_fp16():
-    # C1 is the CPU plumbing config (fp32); its shape runs on the GPU in fp16.
+    # C1 is the CPU plumbing config (fp32); its shape also runs on the GPU in fp16.
     dev = _cuda()
     from grammar.workloads import C1, attention_inputs
     q, k, v = attention_inputs(C1, seed=0, dtype="fp16")
     ref = O.attention(q.float().numpy(), k.float().numpy(), v.float().numpy())
     _check(_run(q.to(dev), k.to(dev), v.to(dev)), ref, "C1@fp16")
+
+
+def test_c1_fp32_as_configured():
+    """C1 exactly as BASELINE.json gives it (B1 H4 N256 d64 fp32) through
+    gr_attn_fwd's fp32 path, at the fp32 bar against the float64 oracle."""
+    dev = _cuda()
+    from grammar.workloads import C1, attention_inputs
+    q, k, v = attention_inputs(C1, seed=0)
+    assert q.dtype == torch.float32
+    ref = O.attention(q.numpy(), k.numpy(), v.numpy(), dtype=np.float64)
+    got = _run(q.to(dev), k.to(dev), v.to(dev)).double().cpu().numpy()
+    print(f"[parity] C1@fp32: max-abs {np.abs(got - ref).max():.2e}", flush=True)
+    assert np.allclose(got, ref, rtol=1e-3, atol=1e-3)
 
 
 def test_c2_full_parity_and_layout_invariance():
