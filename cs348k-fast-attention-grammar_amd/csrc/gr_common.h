@@ -169,6 +169,20 @@ __device__ __forceinline__ void gr_row_load(float (&d)[VEC], const T* p) {
   }
 }
 
+// VEC consecutive elements of a row of a tensor that a split-K GEMM stage
+// left as `parts` fp32 partial products `part_stride` floats apart: their sum.
+template <int VEC>
+__device__ __forceinline__ void gr_row_load_parts(float (&d)[VEC], const float* p, long long part_stride,
+                                                  int parts) {
+  gr_row_load<VEC>(d, p);
+  for (int s = 1; s < parts; ++s) {
+    float e[VEC];
+    gr_row_load<VEC>(e, p + s * part_stride);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) d[k] += e[k];
+  }
+}
+
 template <int VEC, class T>
 __device__ __forceinline__ void gr_row_store(T* p, const float (&y)[VEC]) {
   if constexpr (VEC == 1) {

@@ -156,9 +156,11 @@ __device__ __forceinline__ void gr_gemm_f32_body(const gr_gemm_args& a, char* ld
 
   // lane (l32, g) of block (i, j): row m = wm*WM + 32j + l32, columns
   // n = wn*WN + 32i + 8q + 4g + (0..3) in accumulators 4q..4q+3
-  const float* R = (EPI & GR_EPI_RES) ? static_cast<const float*>(a.r) + z * a.r_sb +
-                                            (long long)tm * BM * a.r_sm + (long long)tn * BN
-                                      : nullptr;
+  // (a null residual adds nothing: a split stage whose sum is taken by its
+  // consumer adds R in its first K part only)
+  const float* R = ((EPI & GR_EPI_RES) && a.r) ? static_cast<const float*>(a.r) + z * a.r_sb +
+                                                     (long long)tm * BM * a.r_sm + (long long)tn * BN
+                                               : nullptr;
 #pragma unroll
   for (int j = 0; j < TM; ++j) {
     const int row = wm * G::WM + j * 32 + l32;
@@ -171,7 +173,9 @@ __device__ __forceinline__ void gr_gemm_f32_body(const gr_gemm_args& a, char* ld
         gr_f32x4 w;
 #pragma unroll
         for (int e = 0; e < 4; ++e) w[e] = gr_epilogue<EPI>(a.alpha * acc[i][j][4 * q + e]);
-        if constexpr ((EPI & GR_EPI_RES) != 0) w += *reinterpret_cast<const gr_f32x4*>(R + (long long)row * a.r_sm + col);
+        if constexpr ((EPI & GR_EPI_RES) != 0) {
+          if (R) w += *reinterpret_cast<const gr_f32x4*>(R + (long long)row * a.r_sm + col);
+        }
         *reinterpret_cast<gr_f32x4*>(crow + col) = w;
       }
   }

@@ -573,7 +573,10 @@ def _match_gemm(loop: ParallelLoop, program: Program):
 def _render_gemm_f32_split(loop, program, f, args, params, km) -> tuple:
     """An fp32 GEMM stage with K split over `ksplit` workgroups: the partial
     products go to a module-scope workspace, and a second launch sums them
-    and applies alpha, the activation and the residual (two plan steps)."""
+    and applies alpha, the activation and the residual (two plan steps).
+    With f["fuse_reduce"] (no activation; every consumer a row-lowered stage
+    that sums the partials as it loads them) there is no second launch: each
+    part applies alpha and the first part adds the residual."""
     ks, M, N, K, batch = f["ksplit"], f["M"], f["N"], f["K"], f["batch"]
     kname = f"{_cname(loop.out)}_kernel"
     rname = f"{_cname(loop.out)}_reduce_kernel"
@@ -587,6 +590,28 @@ def _render_gemm_f32_split(loop, program, f, args, params, km) -> tuple:
   a.c_sb = {f['c_sb']}LL; a.c_sm = {N};
   a.M = {M}; a.N = {N}; a.K = {K};
   a.alpha = {_flt(f['alpha'])};{res_line}"""
+    if f.get("fuse_reduce"):
+        code = f"""
+// stage {loop.out}: fp32 MFMA GEMM {M}x{N}x{K} (x{batch}), tile {f['BM']}x{f['BN']}x{f['BK']}, K split over
+// {ks} workgroups whose partial products (alpha applied, the residual added by the first) stay in this
+// module's workspace: the stages reading {loop.out} sum them as they load it, so two runs of the module
+// must not overlap
+__device__ float {ws}[{ks * batch * M * N}];
+extern "C" __global__ __launch_bounds__({nt})
+void {kname}({params}) {{
+  extern __shared__ __attribute__((aligned(16))) char gr_gemm_smem[];
+{common}
+  a.c = {ws}; a.c_sb = {M * N}LL;
+  if (blockIdx.z != 0) a.r = nullptr;
+  a.ksplit = {ks}; a.c_sz = {batch * M * N}LL;
+  gr_gemm_f32_body<{f['BM']}, {f['BN']}, {f['BK']}, {f['WGM']}, {f['WGN']}, {km}, {f['act']}>(a, gr_gemm_smem);
+}}
+"""
+        grid = (M // f["BM"]) * (N // f["BN"])
+        return code, [{"kernel": kname, "grid": [grid, batch, ks], "block": [nt, 1, 1],
+                       "lds": _gemm_f32_lds(f["BM"], f["BN"], f["BK"], f["kmajor"]), "args": args,
+                       "lowering": "gemm", "tiles": {"block_m": f["BM"], "block_n": f["BN"], "block_k": f["BK"],
+                                                     "ksplit": ks, "sum_in_consumer": True}}]
     code = f"""
 // stage {loop.out}: fp32 MFMA GEMM {M}x{N}x{K} (x{batch}), tile {f['BM']}x{f['BN']}x{f['BK']}, K split over
 // {ks} workgroups; their partial products live in this module's workspace between the two launches,
@@ -769,8 +794,11 @@ def _match_rows(loop: ParallelLoop, program: Program):
 
 
 class _RowGen:
-    def __init__(self, loop, program, f):
+    def __init__(self, loop, program, f, fused=None):
+        """fused: tensor -> (workspace, parts, part stride) for tensors a
+        split-K GEMM stage left as partial products, summed here on load."""
         self.loop, self.p, self.f = loop, program, f
+        self.fused = fused or {}
         self.T = CTYPE[program.dtype]
         self.lines = []
         self.n = 0
@@ -789,6 +817,22 @@ class _RowGen:
     def fresh(self, p):
         self.n += 1
         return f"{p}{self.n}"
+
+    def row_load(self, nm, src):
+        """Statement loading VEC row elements of `src` at column c0 into `nm`."""
+        vec, off = self.f["vec"], self.row_off(src)
+        if src in self.fused:
+            ws, parts, stride = self.fused[src]
+            return f"float {nm}[{vec}]; gr_row_load_parts<{vec}>({nm}, {ws} + {off} + c0, {stride}LL, {parts});"
+        return f"float {nm}[{vec}]; gr_row_load<{vec}>({nm}, t_{src} + {off} + c0);"
+
+    def scalar_load(self, src):
+        """Expression of a per-row scalar of `src` (a [.., 1] tensor)."""
+        off = self.row_off(src)
+        if src in self.fused:
+            ws, parts, stride = self.fused[src]
+            return "(" + " + ".join(f"{ws}[{off} + {s * stride}LL]" for s in range(parts)) + ")"
+        return f"(float)t_{src}[{off}]"
 
     def kind(self, v):
         if isinstance(v, ReductionLoop):
@@ -842,7 +886,7 @@ class _RowGen:
             name = self.reduction([r], emit)[0]
         elif isinstance(v, Load):
             name = self.fresh("s")
-            emit(f"const float {name} = (float)t_{v.source}[{self.row_off(v.source)}];")
+            emit(f"const float {name} = {self.scalar_load(v.source)};")
         else:
             args = [self.scalar(i, emit) for i in v.inputs]
             name = self.fresh("s")
@@ -883,7 +927,7 @@ class _RowGen:
             emit(f"float {acc} = {'-GR_INF' if c.op == 'rowmax' else '0.f'};")
         emit(f"for (int c0 = lane * {vec}; c0 < {C}; c0 += {64 * vec}) {{")
         for src, nm in loads.items():
-            emit(f"  float {nm}[{vec}]; gr_row_load<{vec}>({nm}, t_{src} + {self.row_off(src)} + c0);")
+            emit(f"  {self.row_load(nm, src)}")
         emit(f"#pragma unroll")
         emit(f"  for (int k = 0; k < {vec}; ++k) {{")
         for c, acc, e in zip(cs, accs, exprs):
@@ -914,7 +958,7 @@ class _RowGen:
                 emit(x)
             emit(f"for (int c0 = lane * {vec}; c0 < {C}; c0 += {64 * vec}) {{")
             for src, nm in loads.items():
-                emit(f"  float {nm}[{vec}]; gr_row_load<{vec}>({nm}, t_{src} + {self.row_off(src)} + c0);")
+                emit(f"  {self.row_load(nm, src)}")
             emit(f"  float y[{vec}];")
             emit(f"#pragma unroll")
             emit(f"  for (int k = 0; k < {vec}; ++k) y[k] = {expr};")
@@ -1539,6 +1583,7 @@ def render_module(program: Program, fn_name: str = "fn", check: bool = False) ->
         parts.insert(parts.index('#include "gr_gemm_f32.h"') + 1, '#include "gr_flash_f32.h"')
     steps = []
     over, excess = [], 0
+    matched = []
     for loop in program.body:
         # knobs {"lowering": "generic"} pins a stage to the generic LDS-tile
         # lowering (diagnostics and tests of that lowering)
@@ -1546,13 +1591,16 @@ def render_module(program: Program, fn_name: str = "fn", check: bool = False) ->
         f = None if generic else _match_flash(loop, program)
         gm = _match_gemm(loop, program) if f is None and not generic else None
         rw = _match_rows(loop, program) if f is None and gm is None and not generic else None
+        matched.append((f, gm, rw))
+    fused = _split_sums_in_consumers(program, matched, outputs)
+    for loop, (f, gm, rw) in zip(program.body, matched):
         try:
             if f is not None:
                 code, step = _render_flash(loop, program, f)
             elif gm is not None:
                 code, step = _render_gemm(loop, program, gm)
             elif rw is not None:
-                code, step = _RowGen(loop, program, rw).render()
+                code, step = _RowGen(loop, program, rw, fused).render()
             else:
                 code, step = _StageGen(loop, program, shapes, check=check).render()
         except LdsOverflow as e:
@@ -1569,6 +1617,27 @@ def render_module(program: Program, fn_name: str = "fn", check: bool = False) ->
         plan["check"] = True
     parts.append(f"/*{PLAN_TAG} {json.dumps(plan, sort_keys=True)} {PLAN_TAG}*/")
     return "\n".join(parts) + "\n"
+
+
+def _split_sums_in_consumers(program: Program, matched: list, outputs) -> dict:
+    """Split-K fp32 GEMM stages whose second launch can go: the stage has no
+    activation (a residual is added by its first K part, alpha by every
+    part), its output is an intermediate of the program, and every stage
+    that reads it is row-lowered with rows of the same shape, so those
+    stages sum the partial products as they load them. Marks the GEMM
+    parameters and returns tensor -> (workspace, parts, part stride)."""
+    out = {}
+    for loop, (_, gm, _) in zip(program.body, matched):
+        if not gm or not gm.get("f32") or gm.get("ksplit", 1) <= 1 or (gm["act"] & 3) or loop.out in outputs:
+            continue
+        readers = [(l, rw) for l, (_, _, rw) in zip(program.body, matched)
+                   if l is not loop and any(ld.source == loop.out for ld in _iter_loads(l.body))]
+        if not readers or any(rw is None or tuple(rw["out"]) != tuple(program.tensors[loop.out])
+                              for _, rw in readers):
+            continue
+        gm["fuse_reduce"] = True
+        out[loop.out] = (f"gr_ws_{_cname(loop.out)}", gm["ksplit"], gm["batch"] * gm["M"] * gm["N"])
+    return out
 
 
 def flash_stage_indices(program: Program) -> set:

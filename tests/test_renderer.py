@@ -190,7 +190,10 @@ def test_fp32_gemm_split_k_knob():
     """fp32 GEMM stages offer the schedule knob ksplit: the K loop split over
     workgroups (grid z), the partials in a module-scope workspace, and a
     second launch that sums them and applies alpha, the activation and the
-    residual. A split that does not divide K into whole k tiles keeps one part."""
+    residual. With no activation and only row-lowered readers of the same
+    shape there is no second launch: the first part adds the residual and
+    the reader sums the partials as it loads them. A split that does not
+    divide K into whole k tiles keeps one part."""
     import run_mlp_search as RM
     from grammar import rewrites as R
     from grammar.hip_backend import schedule_knobs
@@ -202,13 +205,27 @@ def test_fp32_gemm_split_k_knob():
     key0 = structural_key(p)
     r.knobs["ksplit"] = 4
     assert structural_key(p) != key0
+    # r = a @ W2 + X, read only by the LayerNorm rows: the sum moves into the reader
     src = emit_module(p)
     steps = [s for s in parse_plan(src)["steps"] if s["kernel"].startswith("t_r_")]
-    assert [s["kernel"] for s in steps] == ["t_r_kernel", "t_r_reduce_kernel"]
+    assert [s["kernel"] for s in steps] == ["t_r_kernel"] and steps[0]["tiles"]["sum_in_consumer"]
     assert steps[0]["grid"] == [(256 // 64) * (512 // 64), 1, 4] and steps[0]["tiles"]["ksplit"] == 4
-    assert steps[1]["merge"] and steps[1]["grid"] == [256 * 512 // 4 // 256, 1, 1]
-    assert "__device__ float gr_ws_t_r[524288];" in src and "gr_gemm_f32_reduce_body<4>(a, gr_ws_t_r, 4" in src
+    body = src.split("void t_r_kernel(")[1].split("}\n")[0]
+    assert "if (blockIdx.z != 0) a.r = nullptr;" in body and "gr_gemm_f32_body<64, 64, 32" in body
+    assert body.rstrip().endswith("4>(a, gr_gemm_smem);")         # the residual epilogue, no activation
+    assert "__device__ float gr_ws_t_r[524288];" in src and "gr_gemm_f32_reduce_body" not in src
+    reader = src.split("void t_out_kernel(")[1]
+    assert "gr_row_load_parts<" in reader and "gr_ws_t_r + " in reader and "131072LL, 4)" in reader
     r.knobs["ksplit"] = 8                       # 1024 / 8 = 128: whole 32-deep k tiles
     assert [s for s in parse_plan(emit_module(p))["steps"] if s["kernel"] == "t_r_kernel"][0]["tiles"]["ksplit"] == 8
+    # a = relu(X @ W1): an activation keeps the second launch
+    q = RM.build_mlp_ln(256, 512, 1024, tile=64)
+    q = R.merge(q, q.body[0], q.body[1])
+    q.body[0].knobs["ksplit"] = 4
+    src = emit_module(q)
+    steps = [s for s in parse_plan(src)["steps"] if s["kernel"].startswith("t_a_")]
+    assert [s["kernel"] for s in steps] == ["t_a_kernel", "t_a_reduce_kernel"]
+    assert steps[1]["merge"] and steps[1]["grid"] == [256 * 1024 // 4 // 256, 1, 1]
+    assert "__device__ float gr_ws_t_a[1048576];" in src and "gr_gemm_f32_reduce_body<1>(a, gr_ws_t_a, 4" in src
     p16 = RM.build_mlp_ln(256, 512, 1024, tile=64, dtype="fp16")
     assert schedule_knobs(p16.body[2], p16) == {}   # fp16 GEMMs take no split

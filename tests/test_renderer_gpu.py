@@ -325,8 +325,11 @@ def test_residual_add_fuses_into_the_gemm(dt):
 @pytest.mark.parametrize("ks_a,ks_r", [(2, 4), (8, 8), (4, 1)])
 def test_fp32_split_k_gemm_stages(ks_a, ks_r):
     """fp32 GEMM stages with K split over workgroups (schedule knob ksplit):
-    the ReLU stage and the residual stage of the merged LN block against the
-    tile interpreter; two runs of the bound plan give the same bits."""
+    the ReLU stage (two launches: the sum applies the activation) and the
+    residual stage of the merged LN block against the tile interpreter; two
+    runs of the bound plan give the same bits. The residual stage, read only
+    by the LayerNorm rows, leaves its sum to them: r is then not materialised
+    and the output carries its check."""
     _cuda()
     import run_mlp_search as RM
     from grammar import rewrites as R
@@ -346,11 +349,14 @@ def test_fp32_split_k_gemm_stages(ks_a, ks_r):
     plan = mod.bind(tensors)
     plan.run()
     torch.cuda.synchronize()
-    first = {n: tensors[n].clone() for n in ("a", "r", "out")}
+    summed_by_reader = [s for s in mod.plan["steps"] if s.get("tiles", {}).get("sum_in_consumer")]
+    assert [s["kernel"] for s in summed_by_reader] == (["t_r_kernel"] if ks_r > 1 else [])
+    names = ("a", "out") if ks_r > 1 else ("a", "r", "out")
+    first = {n: tensors[n].clone() for n in names}
     plan.run()
     torch.cuda.synchronize()
     want = run_program(p, ins)
-    for name in ("a", "r", "out"):
+    for name in names:
         got = tensors[name].cpu().numpy()
         err = float(np.max(np.abs(got - want[name])))
         print(f"[split-k] ksplit {ks_a}/{ks_r} {name}: max|d| {err:.2e}", flush=True)
