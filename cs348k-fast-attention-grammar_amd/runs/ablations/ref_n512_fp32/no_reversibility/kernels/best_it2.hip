@@ -2,8 +2,8 @@
 
 // generated from a grammar program: 8 stage(s), storage fp32
 
-// stage S: fp32 MFMA GEMM 512x512x64 (x1), tile 32x32x32
-extern "C" __global__ __launch_bounds__(64)
+// stage S: fp32 MFMA GEMM 512x512x64 (x1), tile 64x64x32
+extern "C" __global__ __launch_bounds__(256)
 void t_S_kernel(const float* __restrict__ t_Q, const float* __restrict__ t_KT, float* __restrict__ t_S) {
   extern __shared__ __attribute__((aligned(16))) char gr_gemm_smem[];
   gr_gemm_args a;
@@ -13,7 +13,7 @@ void t_S_kernel(const float* __restrict__ t_Q, const float* __restrict__ t_KT, f
   a.c_sb = 262144LL; a.c_sm = 512;
   a.M = 512; a.N = 512; a.K = 64;
   a.alpha = 1.0f;
-  gr_gemm_f32_body<32, 32, 32, 1, 1, false, 0>(a, gr_gemm_smem);
+  gr_gemm_f32_body<64, 64, 32, 2, 2, false, 0>(a, gr_gemm_smem);
 }
 
 
@@ -151,4 +151,4 @@ void t_O_reduce_kernel(const float* __restrict__ t_P, const float* __restrict__ 
   gr_gemm_f32_reduce_body<0>(a, gr_ws_t_O, 4, 32768LL, 1);
 }
 
-/*GR_PLAN {"dtype": "fp32", "fn": "fn", "inputs": ["KT", "Q", "V"], "intermediates": ["P", "S", "Ss", "e", "mx", "sb", "sm"], "meta": {"dtype": "fp32", "flops": 68681728, "flops_exact": true, "inputs": [["KT", [64, 512]], ["Q", [512, 64]], ["V", [512, 64]]], "output": ["O", [512, 64]]}, "outputs": ["O"], "steps": [{"args": ["Q", "KT", "S"], "block": [64, 1, 1], "grid": [256, 1, 1], "kernel": "t_S_kernel", "lds": 19456, "lowering": "gemm", "tiles": {"block_k": 32, "block_m": 32, "block_n": 32}}, {"args": ["S", "Ss"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_Ss_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["Ss", "mx"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_mx_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["Ss", "mx", "sb"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_sb_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["sb", "e"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_e_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["e", "sm"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_sm_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["e", "sm", "P"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_P_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["P", "V", "O"], "block": [64, 1, 1], "grid": [32, 1, 4], "kernel": "t_O_kernel", "lds": 19456, "lowering": "gemm", "tiles": {"block_k": 32, "block_m": 32, "block_n": 32, "ksplit": 4}}, {"args": ["P", "V", "O"], "block": [256, 1, 1], "grid": [32, 1, 1], "kernel": "t_O_reduce_kernel", "lds": 0, "lowering": "gemm", "merge": true}], "tensors": {"KT": [64, 512], "O": [512, 64], "P": [512, 512], "Q": [512, 64], "S": [512, 512], "Ss": [512, 512], "V": [512, 64], "e": [512, 512], "mx": [512, 1], "sb": [512, 512], "sm": [512, 1]}} GR_PLAN*/
+/*GR_PLAN {"dtype": "fp32", "fn": "fn", "inputs": ["KT", "Q", "V"], "intermediates": ["P", "S", "Ss", "e", "mx", "sb", "sm"], "meta": {"dtype": "fp32", "flops": 68681728, "flops_exact": true, "inputs": [["KT", [64, 512]], ["Q", [512, 64]], ["V", [512, 64]]], "output": ["O", [512, 64]]}, "outputs": ["O"], "steps": [{"args": ["Q", "KT", "S"], "block": [256, 1, 1], "grid": [64, 1, 1], "kernel": "t_S_kernel", "lds": 36864, "lowering": "gemm", "tiles": {"block_k": 32, "block_m": 64, "block_n": 64}}, {"args": ["S", "Ss"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_Ss_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["Ss", "mx"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_mx_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["Ss", "mx", "sb"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_sb_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["sb", "e"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_e_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["e", "sm"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_sm_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["e", "sm", "P"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_P_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["P", "V", "O"], "block": [64, 1, 1], "grid": [32, 1, 4], "kernel": "t_O_kernel", "lds": 19456, "lowering": "gemm", "tiles": {"block_k": 32, "block_m": 32, "block_n": 32, "ksplit": 4}}, {"args": ["P", "V", "O"], "block": [256, 1, 1], "grid": [32, 1, 1], "kernel": "t_O_reduce_kernel", "lds": 0, "lowering": "gemm", "merge": true}], "tensors": {"KT": [64, 512], "O": [512, 64], "P": [512, 512], "Q": [512, 64], "S": [512, 512], "Ss": [512, 512], "V": [512, 64], "e": [512, 512], "mx": [512, 1], "sb": [512, 512], "sm": [512, 1]}} GR_PLAN*/

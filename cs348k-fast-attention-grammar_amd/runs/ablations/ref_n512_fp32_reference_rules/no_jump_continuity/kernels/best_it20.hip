@@ -2,8 +2,8 @@
 
 // generated from a grammar program: 5 stage(s), storage fp32
 
-// stage Ss: fp32 MFMA GEMM 512x512x64 (x1), tile 64x32x32
-extern "C" __global__ __launch_bounds__(128)
+// stage Ss: fp32 MFMA GEMM 512x512x64 (x1), tile 32x32x32
+extern "C" __global__ __launch_bounds__(64)
 void t_Ss_kernel(const float* __restrict__ t_Q, const float* __restrict__ t_KT, float* __restrict__ t_Ss) {
   extern __shared__ __attribute__((aligned(16))) char gr_gemm_smem[];
   gr_gemm_args a;
@@ -13,13 +13,13 @@ void t_Ss_kernel(const float* __restrict__ t_Q, const float* __restrict__ t_KT, 
   a.c_sb = 262144LL; a.c_sm = 512;
   a.M = 512; a.N = 512; a.K = 64;
   a.alpha = 0.125f;
-  gr_gemm_f32_body<64, 32, 32, 2, 1, false, 0>(a, gr_gemm_smem);
+  gr_gemm_f32_body<32, 32, 32, 1, 1, false, 0>(a, gr_gemm_smem);
 }
 
 
-// stage e: row lowering (512 rows x 512, one wave per row, 8-wide accesses)
+// stage sb: row lowering (512 rows x 512, one wave per row, 8-wide accesses)
 extern "C" __global__ __launch_bounds__(256)
-void t_e_kernel(const float* __restrict__ t_Ss, float* __restrict__ t_e) {
+void t_sb_kernel(const float* __restrict__ t_Ss, float* __restrict__ t_sb) {
   const int lane = threadIdx.x & 63;
   const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= 512LL) return;
@@ -36,43 +36,48 @@ void t_e_kernel(const float* __restrict__ t_Ss, float* __restrict__ t_e) {
     float x1[8]; gr_row_load<8>(x1, t_Ss + (row / 1LL) * 512LL + c0);
     float y[8];
   #pragma unroll
-    for (int k = 0; k < 8; ++k) y[k] = (__expf((x1[k] - r3)));
+    for (int k = 0; k < 8; ++k) y[k] = (x1[k] - r3);
+    gr_row_store<8>(t_sb + (row / 1LL) * 512LL + c0, y);
+  }
+}
+
+
+// stage e: row lowering (512 rows x 512, one wave per row, 8-wide accesses)
+extern "C" __global__ __launch_bounds__(256)
+void t_e_kernel(const float* __restrict__ t_sb, float* __restrict__ t_e) {
+  const int lane = threadIdx.x & 63;
+  const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= 512LL) return;
+  for (int c0 = lane * 8; c0 < 512; c0 += 512) {
+    float x1[8]; gr_row_load<8>(x1, t_sb + (row / 1LL) * 512LL + c0);
+    float y[8];
+  #pragma unroll
+    for (int k = 0; k < 8; ++k) y[k] = (__expf(x1[k]));
     gr_row_store<8>(t_e + (row / 1LL) * 512LL + c0, y);
   }
 }
 
 
-// stage sm: row lowering (512 rows x 512, one wave per row, 8-wide accesses)
-extern "C" __global__ __launch_bounds__(256)
-void t_sm_kernel(const float* __restrict__ t_e, float* __restrict__ t_sm) {
-  const int lane = threadIdx.x & 63;
-  const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= 512LL) return;
-  float r2 = 0.f;
-  for (int c0 = lane * 8; c0 < 512; c0 += 512) {
-    float x1[8]; gr_row_load<8>(x1, t_e + (row / 1LL) * 512LL + c0);
-  #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      r2 += x1[k];
-    }
-  }
-  r2 = gr_wave_sum(r2);
-  if (lane == 0) t_sm[(row / 1LL) * 1LL] = (float)r2;
-}
-
-
 // stage P: row lowering (512 rows x 512, one wave per row, 8-wide accesses)
 extern "C" __global__ __launch_bounds__(256)
-void t_P_kernel(const float* __restrict__ t_e, const float* __restrict__ t_sm, float* __restrict__ t_P) {
+void t_P_kernel(const float* __restrict__ t_e, float* __restrict__ t_P) {
   const int lane = threadIdx.x & 63;
   const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= 512LL) return;
-  const float s2 = (float)t_sm[(row / 1LL) * 1LL];
+  float r3 = 0.f;
+  for (int c0 = lane * 8; c0 < 512; c0 += 512) {
+    float x2[8]; gr_row_load<8>(x2, t_e + (row / 1LL) * 512LL + c0);
+  #pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      r3 += x2[k];
+    }
+  }
+  r3 = gr_wave_sum(r3);
   for (int c0 = lane * 8; c0 < 512; c0 += 512) {
     float x1[8]; gr_row_load<8>(x1, t_e + (row / 1LL) * 512LL + c0);
     float y[8];
   #pragma unroll
-    for (int k = 0; k < 8; ++k) y[k] = (x1[k] / s2);
+    for (int k = 0; k < 8; ++k) y[k] = (x1[k] / r3);
     gr_row_store<8>(t_P + (row / 1LL) * 512LL + c0, y);
   }
 }
@@ -108,4 +113,4 @@ void t_O_reduce_kernel(const float* __restrict__ t_P, const float* __restrict__ 
   gr_gemm_f32_reduce_body<0>(a, gr_ws_t_O, 8, 32768LL, 1);
 }
 
-/*GR_PLAN {"dtype": "fp32", "fn": "fn", "inputs": ["KT", "Q", "V"], "intermediates": ["P", "Ss", "e", "sm"], "meta": {"dtype": "fp32", "flops": 68681728, "flops_exact": true, "inputs": [["KT", [64, 512]], ["Q", [512, 64]], ["V", [512, 64]]], "output": ["O", [512, 64]]}, "outputs": ["O"], "steps": [{"args": ["Q", "KT", "Ss"], "block": [128, 1, 1], "grid": [128, 1, 1], "kernel": "t_Ss_kernel", "lds": 28672, "lowering": "gemm", "tiles": {"block_k": 32, "block_m": 64, "block_n": 32}}, {"args": ["Ss", "e"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_e_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["e", "sm"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_sm_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["e", "sm", "P"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_P_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["P", "V", "O"], "block": [64, 1, 1], "grid": [32, 1, 8], "kernel": "t_O_kernel", "lds": 19456, "lowering": "gemm", "tiles": {"block_k": 32, "block_m": 32, "block_n": 32, "ksplit": 8}}, {"args": ["P", "V", "O"], "block": [256, 1, 1], "grid": [32, 1, 1], "kernel": "t_O_reduce_kernel", "lds": 0, "lowering": "gemm", "merge": true}], "tensors": {"KT": [64, 512], "O": [512, 64], "P": [512, 512], "Q": [512, 64], "Ss": [512, 512], "V": [512, 64], "e": [512, 512], "sm": [512, 1]}} GR_PLAN*/
+/*GR_PLAN {"dtype": "fp32", "fn": "fn", "inputs": ["KT", "Q", "V"], "intermediates": ["P", "Ss", "e", "sb"], "meta": {"dtype": "fp32", "flops": 68681728, "flops_exact": true, "inputs": [["KT", [64, 512]], ["Q", [512, 64]], ["V", [512, 64]]], "output": ["O", [512, 64]]}, "outputs": ["O"], "steps": [{"args": ["Q", "KT", "Ss"], "block": [64, 1, 1], "grid": [256, 1, 1], "kernel": "t_Ss_kernel", "lds": 19456, "lowering": "gemm", "tiles": {"block_k": 32, "block_m": 32, "block_n": 32}}, {"args": ["Ss", "sb"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_sb_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["sb", "e"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_e_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["e", "P"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_P_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["P", "V", "O"], "block": [64, 1, 1], "grid": [32, 1, 8], "kernel": "t_O_kernel", "lds": 19456, "lowering": "gemm", "tiles": {"block_k": 32, "block_m": 32, "block_n": 32, "ksplit": 8}}, {"args": ["P", "V", "O"], "block": [256, 1, 1], "grid": [32, 1, 1], "kernel": "t_O_reduce_kernel", "lds": 0, "lowering": "gemm", "merge": true}], "tensors": {"KT": [64, 512], "O": [512, 64], "P": [512, 512], "Q": [512, 64], "Ss": [512, 512], "V": [512, 64], "e": [512, 512], "sb": [512, 512]}} GR_PLAN*/

@@ -17,26 +17,37 @@ void t_Ss_kernel(const float* __restrict__ t_Q, const float* __restrict__ t_KT, 
 }
 
 
-// stage sb: row lowering (512 rows x 512, one wave per row, 8-wide accesses)
+// stage mx: row lowering (512 rows x 512, one wave per row, 8-wide accesses)
 extern "C" __global__ __launch_bounds__(256)
-void t_sb_kernel(const float* __restrict__ t_Ss, float* __restrict__ t_sb) {
+void t_mx_kernel(const float* __restrict__ t_Ss, float* __restrict__ t_mx) {
   const int lane = threadIdx.x & 63;
   const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= 512LL) return;
-  float r3 = -GR_INF;
+  float r2 = -GR_INF;
   for (int c0 = lane * 8; c0 < 512; c0 += 512) {
-    float x2[8]; gr_row_load<8>(x2, t_Ss + (row / 1LL) * 512LL + c0);
+    float x1[8]; gr_row_load<8>(x1, t_Ss + (row / 1LL) * 512LL + c0);
   #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      r3 = fmaxf(r3, x2[k]);
+      r2 = fmaxf(r2, x1[k]);
     }
   }
-  r3 = gr_wave_max(r3);
+  r2 = gr_wave_max(r2);
+  if (lane == 0) t_mx[(row / 1LL) * 1LL] = (float)r2;
+}
+
+
+// stage sb: row lowering (512 rows x 512, one wave per row, 8-wide accesses)
+extern "C" __global__ __launch_bounds__(256)
+void t_sb_kernel(const float* __restrict__ t_Ss, const float* __restrict__ t_mx, float* __restrict__ t_sb) {
+  const int lane = threadIdx.x & 63;
+  const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= 512LL) return;
+  const float s2 = (float)t_mx[(row / 1LL) * 1LL];
   for (int c0 = lane * 8; c0 < 512; c0 += 512) {
     float x1[8]; gr_row_load<8>(x1, t_Ss + (row / 1LL) * 512LL + c0);
     float y[8];
   #pragma unroll
-    for (int k = 0; k < 8; ++k) y[k] = (x1[k] - r3);
+    for (int k = 0; k < 8; ++k) y[k] = (x1[k] - s2);
     gr_row_store<8>(t_sb + (row / 1LL) * 512LL + c0, y);
   }
 }
@@ -58,37 +69,26 @@ void t_e_kernel(const float* __restrict__ t_sb, float* __restrict__ t_e) {
 }
 
 
-// stage sm: row lowering (512 rows x 512, one wave per row, 8-wide accesses)
-extern "C" __global__ __launch_bounds__(256)
-void t_sm_kernel(const float* __restrict__ t_e, float* __restrict__ t_sm) {
-  const int lane = threadIdx.x & 63;
-  const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= 512LL) return;
-  float r2 = 0.f;
-  for (int c0 = lane * 8; c0 < 512; c0 += 512) {
-    float x1[8]; gr_row_load<8>(x1, t_e + (row / 1LL) * 512LL + c0);
-  #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      r2 += x1[k];
-    }
-  }
-  r2 = gr_wave_sum(r2);
-  if (lane == 0) t_sm[(row / 1LL) * 1LL] = (float)r2;
-}
-
-
 // stage P: row lowering (512 rows x 512, one wave per row, 8-wide accesses)
 extern "C" __global__ __launch_bounds__(256)
-void t_P_kernel(const float* __restrict__ t_e, const float* __restrict__ t_sm, float* __restrict__ t_P) {
+void t_P_kernel(const float* __restrict__ t_e, float* __restrict__ t_P) {
   const int lane = threadIdx.x & 63;
   const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= 512LL) return;
-  const float s2 = (float)t_sm[(row / 1LL) * 1LL];
+  float r3 = 0.f;
+  for (int c0 = lane * 8; c0 < 512; c0 += 512) {
+    float x2[8]; gr_row_load<8>(x2, t_e + (row / 1LL) * 512LL + c0);
+  #pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      r3 += x2[k];
+    }
+  }
+  r3 = gr_wave_sum(r3);
   for (int c0 = lane * 8; c0 < 512; c0 += 512) {
     float x1[8]; gr_row_load<8>(x1, t_e + (row / 1LL) * 512LL + c0);
     float y[8];
   #pragma unroll
-    for (int k = 0; k < 8; ++k) y[k] = (x1[k] / s2);
+    for (int k = 0; k < 8; ++k) y[k] = (x1[k] / r3);
     gr_row_store<8>(t_P + (row / 1LL) * 512LL + c0, y);
   }
 }
@@ -108,4 +108,4 @@ void t_O_kernel(const float* __restrict__ t_P, const float* __restrict__ t_V, fl
   gr_gemm_f32_body<32, 32, 32, 1, 1, false, 0>(a, gr_gemm_smem);
 }
 
-/*GR_PLAN {"dtype": "fp32", "fn": "fn", "inputs": ["KT", "Q", "V"], "intermediates": ["P", "Ss", "e", "sb", "sm"], "meta": {"dtype": "fp32", "flops": 68681728, "flops_exact": true, "inputs": [["KT", [64, 512]], ["Q", [512, 64]], ["V", [512, 64]]], "output": ["O", [512, 64]]}, "outputs": ["O"], "steps": [{"args": ["Q", "KT", "Ss"], "block": [64, 1, 1], "grid": [256, 1, 1], "kernel": "t_Ss_kernel", "lds": 19456, "lowering": "gemm", "tiles": {"block_k": 32, "block_m": 32, "block_n": 32}}, {"args": ["Ss", "sb"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_sb_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["sb", "e"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_e_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["e", "sm"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_sm_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["e", "sm", "P"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_P_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["P", "V", "O"], "block": [64, 1, 1], "grid": [32, 1, 1], "kernel": "t_O_kernel", "lds": 19456, "lowering": "gemm", "tiles": {"block_k": 32, "block_m": 32, "block_n": 32}}], "tensors": {"KT": [64, 512], "O": [512, 64], "P": [512, 512], "Q": [512, 64], "Ss": [512, 512], "V": [512, 64], "e": [512, 512], "sb": [512, 512], "sm": [512, 1]}} GR_PLAN*/
+/*GR_PLAN {"dtype": "fp32", "fn": "fn", "inputs": ["KT", "Q", "V"], "intermediates": ["P", "Ss", "e", "mx", "sb"], "meta": {"dtype": "fp32", "flops": 68681728, "flops_exact": true, "inputs": [["KT", [64, 512]], ["Q", [512, 64]], ["V", [512, 64]]], "output": ["O", [512, 64]]}, "outputs": ["O"], "steps": [{"args": ["Q", "KT", "Ss"], "block": [64, 1, 1], "grid": [256, 1, 1], "kernel": "t_Ss_kernel", "lds": 19456, "lowering": "gemm", "tiles": {"block_k": 32, "block_m": 32, "block_n": 32}}, {"args": ["Ss", "mx"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_mx_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["Ss", "mx", "sb"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_sb_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["sb", "e"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_e_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["e", "P"], "block": [256, 1, 1], "grid": [128, 1, 1], "kernel": "t_P_kernel", "lds": 0, "lowering": "rows", "tiles": {"vec": 8}}, {"args": ["P", "V", "O"], "block": [64, 1, 1], "grid": [32, 1, 1], "kernel": "t_O_kernel", "lds": 19456, "lowering": "gemm", "tiles": {"block_k": 32, "block_m": 32, "block_n": 32}}], "tensors": {"KT": [64, 512], "O": [512, 64], "P": [512, 512], "Q": [512, 64], "Ss": [512, 512], "V": [512, 64], "e": [512, 512], "mx": [512, 1], "sb": [512, 512]}} GR_PLAN*/
