@@ -187,3 +187,68 @@ def test_evaluator_checking_build_gate(tmp_path, monkeypatch):
         assert st["checked_builds"] == 1 and st["check_findings"] == 0 and st["timed_variants"] == 1
     finally:
         ev.close()
+
+
+def _ln_block_f64(x, w1, w2, eps=1e-5):
+    """relu(X W1) W2 + X, then LayerNorm over the row without an affine part,
+    in float64 (run_mlp_search.py:138-149)."""
+    x, w1, w2 = (np.asarray(t, dtype=np.float64) for t in (x, w1, w2))
+    r = np.maximum(x @ w1, 0.0) @ w2 + x
+    mu = r.mean(axis=1, keepdims=True)
+    var = ((r - mu) ** 2).mean(axis=1, keepdims=True)
+    return (r - mu) / np.sqrt(var + eps)
+
+
+def test_committed_ln_block_program_vs_closed_form():
+    """The descent-found reference MLP + LayerNorm block (runs/mlp_ln_best.json:
+    split-K fp32 GEMMs whose partial products the row stages sum on load),
+    run twice in a row (the second run must not see the first one's partials
+    twice) against the float64 closed form at the reference's 1e-3 bar."""
+    dev = _cuda()
+    import run_mlp_search as RM
+    from grammar.hip_module import HipModule
+    from grammar.kernel_ast import emit_module
+    prog, saved = _load("mlp_ln_best.json")
+    _case(f"committed LN block program {saved['stages']}")
+    mod = HipModule(emit_module(prog))
+    steps = mod.plan["steps"]
+    print(f"[plan] {[(s['lowering'], s.get('tiles', {}).get('ksplit')) for s in steps]}", flush=True)
+    named = RM.mlp_inputs(256, 512, 1024, "fp32", seed=5, device="cpu")
+    want = _ln_block_f64(named["X"].numpy(), named["W1"].numpy(), named["W2"].numpy())
+    args = [named[n].to(dev) for n in mod.inputs]
+    first = mod.fn(*args)
+    torch.cuda.synchronize()
+    first = first.cpu().numpy()
+    second = mod.fn(*args).cpu().numpy()
+    for got, what in ((first, "first run"), (second, "second run")):
+        err = float(np.max(np.abs(got - want)))
+        print(f"[check] LN block {what}: max-abs {err:.3e}", flush=True)
+        assert np.isfinite(err) and err <= 1e-3, (what, err)
+    # LayerNorm rows: mean 0 and variance var/(var+eps) ~ 1
+    assert np.max(np.abs(first.mean(axis=1))) < 1e-4
+
+
+@pytest.mark.parametrize("rules", ["ref_n512_fp32", "ref_n512_fp32_reference_rules"])
+def test_committed_reference_workload_best_vs_oracle(rules):
+    """The durable best kernel of the full-rule descent at the reference's own
+    workload (one head, N = 512, d = 64, fp32; runs/ablations/<rules>/full),
+    loaded from its committed .hip as bench.py --kernel loads it, against the
+    float64 oracle at the reference's 1e-3 bar (run_attention_search.py:160-181)."""
+    dev = _cuda()
+    import glob
+    import re
+    from grammar.hip_module import HipModule
+    kdir = os.path.join(PKG, "runs", "ablations", rules, "full", "kernels")
+    last = max(glob.glob(os.path.join(kdir, "best_it*.hip")), key=lambda p: int(re.findall(r"\d+", os.path.basename(p))[0]))
+    _case(f"reference-workload best {rules}: {os.path.basename(last)}")
+    with open(last) as f:
+        mod = HipModule(f.read())
+    g = torch.Generator("cpu").manual_seed(21)
+    ins = {n: torch.randn(tuple(s), generator=g) for n, s in mod.KERNEL_META["inputs"]}
+    out = mod.fn(*[ins[n].to(dev) for n in mod.inputs])
+    torch.cuda.synchronize()
+    q, kt, v = (ins[n].double().numpy() for n in ("Q", "KT", "V"))
+    ref = O.attention(q, kt, v, k_transposed=True, dtype=np.float64)
+    err = float(np.max(np.abs(out.double().cpu().numpy() - ref)))
+    print(f"[check] {rules} {[s['lowering'] for s in mod.plan['steps']]}: max-abs {err:.3e}", flush=True)
+    assert np.isfinite(err) and err <= 1e-3
