@@ -4,6 +4,7 @@
 
 #include <cstdint>
 #include <mutex>
+#include <vector>
 
 #include "gr_flash_decode.h"
 #include "gr_flash_f32.h"
@@ -229,13 +230,96 @@ __global__ void gr_selftest_mfma32_kernel(const _Float16* A, const _Float16* B, 
 namespace {
 
 // fp32 (the reference's own dtype) on the fp32 matrix cores: a workgroup owns
-// 32 queries and splits all N keys over its NW waves (merged through LDS), so
-// one launch suffices and no workspace is needed.
+// 32 queries and splits its keys over its NW waves (merged through LDS). When
+// the query blocks alone would leave most CUs idle, the keys of each query
+// block are also split over PARTS workgroups (PARTS = 1: one launch, no
+// workspace).
 template <int D, int NW, bool KT>
 __global__ __launch_bounds__(NW * 64) void gr_flash32_kernel(gr_attn_args a, int nkb) {
   extern __shared__ __attribute__((aligned(16))) char gr_lds[];
   gr_flash32_fwd_body<D, 32, NW, KT, 1>(a, gr_lds, nullptr, nullptr, nkb);
 }
+
+// ONE: one 32-key block per wave, known at compile time (no block loop and no
+// prefetch registers); else nkb blocks per wave.
+template <int D, bool KT, int PARTS, bool ONE>
+__global__ __launch_bounds__(256) void gr_flash32_split_kernel(gr_attn_args a, int nkb, float* ws_o, float* ws_ml) {
+  extern __shared__ __attribute__((aligned(16))) char gr_lds[];
+  gr_flash32_fwd_body<D, 32, 4, KT, PARTS>(a, gr_lds, ws_o, ws_ml, ONE ? 0 : nkb);
+}
+
+template <int D, int PARTS>
+__global__ __launch_bounds__(256) void gr_flash32_merge_kernel(gr_attn_args a, const float* ws_o, const float* ws_ml) {
+  gr_flash32_merge_body<D, PARTS>(a, ws_o, ws_ml);
+}
+
+// Workspace of the fp32 key split: one buffer per (device, stream), grown on
+// demand. Calls on one stream run in order, so they can share it; a buffer
+// that grew is kept (queued work may still read it) until the process ends.
+// Only problems of at most 256 query blocks split, so a buffer stays below
+// 256 * 32 rows * 8 parts * (D + 2) floats (34 MiB at D = 128).
+struct F32Workspace {
+  int dev;
+  hipStream_t st;
+  void* p;
+  size_t bytes;
+};
+std::mutex g_f32_ws_lock;
+std::vector<F32Workspace> g_f32_ws;
+std::vector<void*> g_f32_ws_retired;
+
+int f32_workspace(hipStream_t st, size_t bytes, void** out) {
+  int dev = 0;
+  int rc = gr::hip_check(hipGetDevice(&dev), GR_E_RUNTIME, "gr_attn_fwd: hipGetDevice");
+  if (rc) return rc;
+  std::lock_guard<std::mutex> hold(g_f32_ws_lock);
+  F32Workspace* w = nullptr;
+  for (auto& e : g_f32_ws)
+    if (e.dev == dev && e.st == st) w = &e;
+  if (w && w->bytes >= bytes) {
+    *out = w->p;
+    return GR_OK;
+  }
+  void* p = nullptr;
+  rc = gr::hip_check(hipMalloc(&p, bytes), GR_E_RUNTIME, "gr_attn_fwd: fp32 key-split workspace");
+  if (rc) return rc;
+  if (w) {
+    g_f32_ws_retired.push_back(w->p);
+    w->p = p;
+    w->bytes = bytes;
+  } else {
+    g_f32_ws.push_back({dev, st, p, bytes});
+  }
+  *out = p;
+  return GR_OK;
+}
+
+template <int D, bool KT, int PARTS>
+int launch_flash32_split(const gr_attn_args& a, long long nblk, hipStream_t st) {
+  const long long rows = (long long)a.B * a.H * a.N;
+  const size_t o_floats = (size_t)PARTS * rows * D;
+  void* ws = nullptr;
+  int rc = f32_workspace(st, (o_floats + (size_t)PARTS * rows * 2) * sizeof(float), &ws);
+  if (rc) return rc;
+  float* ws_o = static_cast<float*>(ws);
+  float* ws_ml = ws_o + o_floats;
+  const int nkb = a.N / (32 * 4 * PARTS);
+  if (nkb == 1)
+    hipLaunchKernelGGL((gr_flash32_split_kernel<D, KT, PARTS, true>), dim3((unsigned)(nblk * PARTS)), dim3(256),
+                       (gr_flash32_lds<D, 4>::BYTES), st, a, nkb, ws_o, ws_ml);
+  else
+    hipLaunchKernelGGL((gr_flash32_split_kernel<D, KT, PARTS, false>), dim3((unsigned)(nblk * PARTS)), dim3(256),
+                       (gr_flash32_lds<D, 4>::BYTES), st, a, nkb, ws_o, ws_ml);
+  rc = gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_fwd fp32 key-split launch");
+  if (rc) return rc;
+  const long long threads = rows * (D / 8);
+  hipLaunchKernelGGL((gr_flash32_merge_kernel<D, PARTS>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                     a, (const float*)ws_o, (const float*)ws_ml);
+  return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_fwd fp32 merge launch");
+}
+
+// Workgroups a split launch aims for: one per CU of an MI355X.
+constexpr long long kF32SplitTarget = 256;
 
 template <int D, bool KT>
 int launch_flash32(const gr_attn_args& a, hipStream_t st) {
@@ -243,6 +327,13 @@ int launch_flash32(const gr_attn_args& a, hipStream_t st) {
   const int nkb = a.N / (32 * nw);
   const long long nblk = (long long)a.B * a.H * (a.N / 32);
   if (nblk <= 0 || nblk > 0x7fffffffLL) return gr::fail(GR_E_ARG, "gr_attn_fwd: grid size %lld out of range", nblk);
+  // the most key parts (8, 4 or 2, dividing the 32-key blocks of a wave)
+  // that keep the launch within one workgroup per CU
+  if (nw == 4) {
+    if (nkb % 8 == 0 && nblk * 8 <= kF32SplitTarget) return launch_flash32_split<D, KT, 8>(a, nblk, st);
+    if (nkb % 4 == 0 && nblk * 4 <= kF32SplitTarget) return launch_flash32_split<D, KT, 4>(a, nblk, st);
+    if (nkb % 2 == 0 && nblk * 2 <= kF32SplitTarget) return launch_flash32_split<D, KT, 2>(a, nblk, st);
+  }
   if (nw == 4)
     hipLaunchKernelGGL((gr_flash32_kernel<D, 4, KT>), dim3((unsigned)nblk), dim3(256), (gr_flash32_lds<D, 4>::BYTES),
                        st, a, nkb);

@@ -18,7 +18,8 @@
 // (gr_flash32_merge_body) combines them,
 //   O = sum_s 2^((m_s - M) c) O_s / sum_s 2^((m_s - M) c) l_s,  M = max_s m_s.
 // The workspace is module-scope device arrays the renderer sizes for the
-// stage; two launches of one module must not overlap.
+// stage (two launches of one module must not overlap), or, behind
+// gr_attn_fwd, a buffer the library keeps per (device, stream).
 //
 //  * Transposed form as in gr_flash_fwd_body: S^T = K Q^T, O^T = V^T P^T. A
 //    32x32x2 MFMA contracts one index per half-wave: for d the lane of half g
@@ -39,7 +40,7 @@ struct gr_flash32_lds {
 };
 
 // nkb: 32-key blocks per wave when the chunk length is only known at run time
-// (the library launch, PARTS = 1: nkb = N / (32 NW)); 0 takes BN / 32.
+// (the library launches: nkb = N / (32 NW PARTS)); 0 takes BN / 32.
 template <int D, int BN, int NW, bool KT_LAYOUT, int PARTS>
 __device__ __forceinline__ void gr_flash32_fwd_body(const gr_attn_args& a, char* lds, float* ws_o, float* ws_ml,
                                                     int nkb = 0) {
@@ -70,15 +71,19 @@ __device__ __forceinline__ void gr_flash32_fwd_body(const gr_attn_args& a, char*
   for (int dg = 0; dg < DG; ++dg)
     qf[dg] = *reinterpret_cast<const gr_f32x4*>(Qp + (long long)(q0 + l32) * a.q_sn + 8 * dg + 4 * g);
 
-  // operands of one 32-key block: K (MFMA A of the scores) and V (MFMA A of P V)
+  // operands of one 32-key block: K (MFMA A of the scores) and V (MFMA A of P V).
+  // Each lane keeps one base pointer per operand; the rest of every address
+  // is wave-uniform (scalar arithmetic when the strides are run-time values).
+  const float* const k_lane = KT_LAYOUT ? Kp + (long long)(4 * g) * a.k_sn + l32 : Kp + (long long)l32 * a.k_sn + 4 * g;
+  const float* const v_lane = Vp + (long long)(4 * g) * a.v_sn + l32;
   auto load_k = [&](int kr, gr_f32x4 (&kf)[DG]) {
 #pragma unroll
     for (int dg = 0; dg < DG; ++dg) {
       if constexpr (KT_LAYOUT) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) kf[dg][t] = Kp[(long long)(8 * dg + 4 * g + t) * a.k_sn + kr + l32];
+        for (int t = 0; t < 4; ++t) kf[dg][t] = k_lane[(long long)(8 * dg + t) * a.k_sn + kr];
       } else {
-        kf[dg] = *reinterpret_cast<const gr_f32x4*>(Kp + (long long)(kr + l32) * a.k_sn + 8 * dg + 4 * g);
+        kf[dg] = *reinterpret_cast<const gr_f32x4*>(k_lane + (long long)kr * a.k_sn + 8 * dg);
       }
     }
   };
@@ -86,8 +91,7 @@ __device__ __forceinline__ void gr_flash32_fwd_body(const gr_attn_args& a, char*
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int t = 0; t < 16; ++t)
-        vf[db][t] = Vp[(long long)(kr + 8 * (t >> 2) + 4 * g + (t & 3)) * a.v_sn + 32 * db + l32];
+      for (int t = 0; t < 16; ++t) vf[db][t] = v_lane[(long long)(kr + 8 * (t >> 2) + (t & 3)) * a.v_sn + 32 * db];
   };
 
   gr_f32x16 o[DB];

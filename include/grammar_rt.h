@@ -110,8 +110,14 @@ int gr_plan_time(gr_plan* p, void* stream, int warmup, int iters, int mode, floa
  *  default 1/sqrt(D) with D >= 3), and a larger fp16 scale is refused with
  *  GR_E_ARG (bf16 takes any scale). GR_F32 (the reference's own dtype, fp32
  *  throughout on the fp32 matrix cores): non-causal only, N a multiple of 32,
- *  block_m and block_n ignored (a workgroup owns 32 queries and splits all N
- *  keys over its waves); not for gr_attn_fwd_train.
+ *  block_m and block_n ignored (a workgroup owns 32 queries and splits its
+ *  keys over its waves); not for gr_attn_fwd_train. When B * H * N / 32 query
+ *  blocks would leave CUs idle (N a multiple of 256, at most 128 blocks), the
+ *  keys of a query block are also split over 2, 4 or 8 workgroups and a
+ *  second launch merges their partials, which sit in a workspace the library
+ *  allocates once per (device, stream) and grows on demand (a grown buffer is
+ *  kept until the process ends; at most 34 MiB): call once on a stream
+ *  before capturing such calls into a graph.
  *  Q, V, O: [B, H, N, D] with strides {batch, head, seq} in elements
  *  (unit stride along D). K: [B, H, N, D] if k_transposed == 0, else KT
  *  [B, H, D, N] whose k_strides = {batch, head, d} (unit stride along N).

@@ -175,6 +175,12 @@ F32 = [
     (1, 2, 192, 64, True),
     (1, 1, 96, 128, False),
     (2, 1, 32, 64, False),
+    # the keys of each query block also split over workgroups when the query
+    # blocks would leave CUs idle: 4 parts, 2 parts (above), 8 parts, 2 parts
+    # at 128 query blocks, and 512 query blocks without a split
+    (1, 1, 1024, 64, False),
+    (1, 2, 2048, 128, True),
+    (4, 8, 512, 64, False),
 ]
 
 
@@ -192,6 +198,53 @@ def test_attention_fp32_parity(case):
     o = _run(q.to(dev), k.to(dev), v.to(dev), k_transposed=kt)
     got = o.double().cpu().numpy()
     print(f"[parity] fp32 {case}: max-abs {np.abs(got - ref).max():.2e}", flush=True)
+    assert np.allclose(got, ref, rtol=1e-3, atol=1e-3)
+
+
+def test_attention_fp32_key_split_workspace_per_stream():
+    """The fp32 key split keeps its partials in a library workspace per
+    (device, stream) that grows on demand: a split call, a larger one queued
+    behind it on the same stream (the workspace grows while the first may
+    still run), and a split call on a second stream, with no synchronisation
+    in between; each against the float64 oracle."""
+    dev = _cuda()
+    from grammar.attention import flash_attention_fwd
+    cases = [(1, 1, 512, 64), (2, 2, 1024, 128), (1, 1, 256, 64)]
+    g = torch.Generator("cpu").manual_seed(9)
+    ins = [tuple(torch.randn(B, H, N, D, generator=g) for _ in range(3)) for B, H, N, D in cases]
+    dev_ins = [tuple(t.to(dev) for t in x) for x in ins]
+    torch.cuda.synchronize()
+    outs = [flash_attention_fwd(*dev_ins[0]), flash_attention_fwd(*dev_ins[1])]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        outs.append(flash_attention_fwd(*dev_ins[2]))
+    torch.cuda.synchronize()
+    for (q, k, v), o, c in zip(ins, outs, cases):
+        ref = O.attention(q.numpy(), k.numpy(), v.numpy(), dtype=np.float64)
+        got = o.double().cpu().numpy()
+        print(f"[parity] fp32 split {c}: max-abs {np.abs(got - ref).max():.2e}", flush=True)
+        assert np.allclose(got, ref, rtol=1e-3, atol=1e-3), c
+
+
+@pytest.mark.parametrize("B,H,n", [(1, 2, 512), (2, 8, 2048)])
+def test_attention_fp32_strided_heads(B, H, n):
+    """fp32 with Q, K, V and O read and written through [B, N, H, D] storage
+    (head stride D, sequence stride H * D), split (32 query blocks: 4 key
+    parts) and unsplit with 16 32-key blocks per wave (1,024 query blocks),
+    against the float64 oracle."""
+    dev = _cuda()
+    from grammar.attention import flash_attention_fwd
+    D = 64
+    g = torch.Generator("cpu").manual_seed(13)
+    q, k, v = (torch.randn(B, n, H, D, generator=g) for _ in range(3))
+    qd, kd, vd = (t.to(dev).transpose(1, 2) for t in (q, k, v))
+    out = torch.empty(B, n, H, D, device=dev).transpose(1, 2)
+    o = flash_attention_fwd(qd, kd, vd, out=out)
+    torch.cuda.synchronize()
+    ref = O.attention(*(t.transpose(1, 2).numpy() for t in (q, k, v)), dtype=np.float64)
+    got = o.double().cpu().numpy()
+    print(f"[parity] fp32 strided N={n}: max-abs {np.abs(got - ref).max():.2e}", flush=True)
     assert np.allclose(got, ref, rtol=1e-3, atol=1e-3)
 
 
