@@ -4,7 +4,7 @@ fp16 MFMA peak on one MI355X at B=4, H=16, N=1024, d=64 (BASELINE.json
 config C2), with the descent's evals/min measured in the same run.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2|C3]
-                    [--search-seconds S] [--kernel descent|handwritten]
+                    [--search-seconds S] [--kernel descent|handwritten|fp32|PATH]
 
 1. Descent: the stochastic rewrite descent runs from the naive 8-stage
    attention program (every stage its own kernel, full-extent tiles) for at
@@ -490,8 +490,9 @@ def main() -> int:
     ap.add_argument("--config", default="C2", choices=["C2", "C3"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--kernel", default="descent",
-                    help="descent | handwritten | PATH of a saved module (.hip as RunLogger writes it, or a "
-                         ".json holding a program key): re-time that module alone (reference bench.py --kernel)")
+                    help="descent | handwritten | fp32 (only the fp32 configs through gr_attn_fwd) | PATH of a "
+                         "saved module (.hip as RunLogger writes it, or a .json holding a program key): re-time "
+                         "that module alone (reference bench.py --kernel)")
     ap.add_argument("--search-seconds", type=float, default=60.0, dest="search_seconds",
                     help="wall budget of the live descent (0 = use the committed best program)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -531,6 +532,9 @@ def main() -> int:
         log(f"[bench] copy calibration: {args.steps} copies of {args.copy_calibration} MiB")
         return 0
 
+    if args.kernel == "fp32":
+        print(json.dumps(fp32_attention(args.steps, args.seed)), flush=True)
+        return 0
     if args.kernel not in ("descent", "handwritten"):
         print(json.dumps(bench_module(args.kernel, args.steps, args.warmup, args.seed)), flush=True)
         return 0
