@@ -4,6 +4,7 @@
 
 #include <cstdint>
 #include <mutex>
+#include <thread>
 #include <vector>
 
 #include "gr_flash_decode.h"
@@ -256,11 +257,14 @@ __global__ __launch_bounds__(256) void gr_flash32_merge_kernel(gr_attn_args a, c
 // Workspace of the fp32 key split: one buffer per (device, stream), grown on
 // demand. Calls on one stream run in order, so they can share it; a buffer
 // that grew is kept (queued work may still read it) until the process ends.
-// Only problems of at most 256 query blocks split, so a buffer stays below
-// 256 * 32 rows * 8 parts * (D + 2) floats (34 MiB at D = 128).
+// hipStreamPerThread names a different stream in every host thread, so its
+// buffers are kept per thread as well. Only problems of at most 256 query
+// blocks split, so a buffer stays below 256 * 32 rows * 8 parts * (D + 2)
+// floats (34 MiB at D = 128).
 struct F32Workspace {
   int dev;
   hipStream_t st;
+  std::thread::id thread;
   void* p;
   size_t bytes;
 };
@@ -272,10 +276,11 @@ int f32_workspace(hipStream_t st, size_t bytes, void** out) {
   int dev = 0;
   int rc = gr::hip_check(hipGetDevice(&dev), GR_E_RUNTIME, "gr_attn_fwd: hipGetDevice");
   if (rc) return rc;
+  const std::thread::id thread = st == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
   std::lock_guard<std::mutex> hold(g_f32_ws_lock);
   F32Workspace* w = nullptr;
   for (auto& e : g_f32_ws)
-    if (e.dev == dev && e.st == st) w = &e;
+    if (e.dev == dev && e.st == st && e.thread == thread) w = &e;
   if (w && w->bytes >= bytes) {
     *out = w->p;
     return GR_OK;
@@ -288,7 +293,7 @@ int f32_workspace(hipStream_t st, size_t bytes, void** out) {
     w->p = p;
     w->bytes = bytes;
   } else {
-    g_f32_ws.push_back({dev, st, p, bytes});
+    g_f32_ws.push_back({dev, st, thread, p, bytes});
   }
   *out = p;
   return GR_OK;
