@@ -250,11 +250,11 @@ class Evaluator:
         timed; hiprtc_compiles and code_cache_hits split where their code
         objects came from; memo_hits are programs already scored."""
         el = max(1e-9, time.time() - self.t_start)
-        return {"compiled_variants": self._compiles, "hiprtc_compiles": self._compiles,
+        return {"hiprtc_compiles": self._compiles,
                 "code_cache_hits": self._code_hits, "compile_timeouts": self._timeouts,
                 "nondeterministic": self._nondeterministic, "checked_builds": self._checked,
                 "check_findings": self._check_findings, "timed_variants": self._runs,
-                "cache_hits": self._cache_hits, "memo_hits": self._cache_hits,
+                "memo_hits": self._cache_hits,
                 "distinct_scored": len(self._cache), "wall_s": el, "evals_per_min": 60.0 * self._runs / el}
 
     # ---- scoring -------------------------------------------------------------

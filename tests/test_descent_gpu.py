@@ -148,6 +148,53 @@ def test_live_descent_finds_a_kernel_that_passes_the_oracle(tmp_path, monkeypatc
         ev.close()
 
 
+def test_c5_descent_at_its_own_workload(tmp_path, monkeypatch):
+    """C5 as configured: the descent from the naive 8-stage program at
+    B4 H16 N1024 d64 fp16, 500 iterations (Stage 2 every 4, K = 5) with a
+    60 s budget and an empty code-object cache, then the reference's final
+    step: its best program checked against the closed form
+    (run_attention_search.py:235-271, verify at :169-181). Here the refined
+    best also runs on all 64 heads against the CPU oracle."""
+    import time
+    dev = _cuda()
+    monkeypatch.setenv("GR_CACHE_DIR", str(tmp_path / "co"))
+    import run_attention_search as RS
+    from grammar.hip_module import HipModule
+    from grammar.kernel_ast import emit_module
+    from grammar.optimization import EvalConfig, Evaluator, SearchConfig, autotune
+    from grammar.workloads import C2, attention_inputs
+    prog = RS.build_attention(1024, 64, B=4, H=16, dtype="fp16")
+    _case("C5 descent B4 H16 N1024 d64 fp16, 500 iterations, 60 s budget, empty code-object cache")
+    budget = 60.0
+    ev = Evaluator(EvalConfig(seed=0), reference=RS.attention_reference(1.0 / math.sqrt(64)))
+    try:
+        t0 = time.time()
+        best = autotune(prog, ev, SearchConfig(iters=500, N=4, K=5, seed=0, verbose=False, time_budget_s=budget))
+        wall = time.time() - t0
+        st = ev.stats()
+        rate = 60.0 * st["timed_variants"] / wall
+        print(f"[descent] C5: {ev.iterations} iterations in {wall:.1f} s, {st['timed_variants']} timed, "
+              f"{st['hiprtc_compiles']} compiles, {st['code_cache_hits']} code-cache hits, {rate:.0f} evals/min",
+              flush=True)
+        assert ev.iterations == 500 or wall >= budget
+        assert st["timed_variants"] > 0 and st["hiprtc_compiles"] > 0
+        assert rate >= 30.0, rate
+        assert ev(best) < 1e9
+        best, finalists = ev.refine(k=6)
+        print(f"[refine] {[(r['stages'], round(r['refined_ms'] * 1e3, 2)) for r in finalists]}", flush=True)
+    finally:
+        ev.close()
+    # the reference's final verify (seeded inputs, torch closed form on the GPU)
+    assert RS.verify(best, 1024, 64)
+    q, k, v = attention_inputs(C2, seed=0)
+    kt = k.transpose(-1, -2).contiguous()
+    mod = HipModule(emit_module(best))
+    out = mod.fn(kt.to(dev), q.to(dev), v.to(dev))
+    torch.cuda.synchronize()
+    ref = O.attention(q.float().numpy(), kt.float().numpy(), v.float().numpy(), k_transposed=True)
+    _check(out, ref, "C5 descent best (all 64 heads)")
+
+
 def test_evaluator_rejects_a_variant_that_fails_the_checker(tmp_path, monkeypatch):
     _cuda()
     monkeypatch.setenv("GR_CACHE_DIR", str(tmp_path / "co"))
