@@ -57,6 +57,40 @@ int dispatch_tiles(const gr_attn_args& a, int bm, int bn, hipStream_t st) {
   return gr::fail(GR_E_ARG, "gr_attn_fwd: unsupported tile (block_m=%d, block_n=%d) for D=%d", bm, bn, D);
 }
 
+// fp16 with scale log2(e) > 1 (Q as given, every score scaled on the VALU):
+// one tile, 64 queries x 32 keys (two waves).
+template <int D, bool CAUSAL, bool KT>
+int launch_unscaled_q(const gr_attn_args& a, hipStream_t st) {
+  constexpr int BM = 64, BN = 32, NW = 2;
+  constexpr bool DIRECT = (D * BN / 8) % (NW * 64) == 0;
+  constexpr int LDS = gr_flash_lds<D, BN>::BYTES;
+  if (a.N % BM != 0)
+    return gr::fail(GR_E_ARG, "gr_attn_fwd: fp16 with scale * log2(e) > 1 needs N=%d a multiple of 64", a.N);
+  const long long nblk = (long long)a.B * a.H * (a.N / BM);
+  if (nblk <= 0 || nblk > 0x7fffffffLL) return gr::fail(GR_E_ARG, "gr_attn_fwd: grid size %lld out of range", nblk);
+  hipLaunchKernelGGL((gr_flash_fwd_kernel<_Float16, D, BN, NW, 1, CAUSAL, KT, false, true, DIRECT, false, false>),
+                     dim3((unsigned)nblk), dim3(NW * 64), LDS, st, a);
+  return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_fwd launch");
+}
+
+int dispatch_unscaled_q(const gr_attn_args& a, int D, bool causal, bool kt, int bm, int bn, hipStream_t st) {
+  if ((bm != 0 && bm != 64) || (bn != 0 && bn != 32))
+    return gr::fail(GR_E_ARG, "gr_attn_fwd: fp16 with scale * log2(e) > 1 runs the 64 x 32 tile only (asked for %d x %d)",
+                    bm, bn);
+#define GR_CASE(DD, C, K) \
+  if (D == DD && causal == C && kt == K) return launch_unscaled_q<DD, C, K>(a, st);
+  GR_CASE(64, false, false)
+  GR_CASE(64, false, true)
+  GR_CASE(64, true, false)
+  GR_CASE(64, true, true)
+  GR_CASE(128, false, false)
+  GR_CASE(128, false, true)
+  GR_CASE(128, true, false)
+  GR_CASE(128, true, true)
+#undef GR_CASE
+  return gr::fail(GR_E_ARG, "gr_attn_fwd: head dim D=%d unsupported (64 or 128)", D);
+}
+
 template <class T>
 int dispatch_shape(const gr_attn_args& a, int D, bool causal, bool kt, int bm, int bn, hipStream_t st) {
 #define GR_CASE(DD, C, K)                                                          \
@@ -115,10 +149,10 @@ __global__ __launch_bounds__(256) void gr_attn_combine_kernel(const float* __res
   gr_st16(o + b * o_sb + h * o_sh + (long long)q * o_sn + ch * 8, out);
 }
 
-template <class T, int D, int BN, int NW, bool SPLIT>
+template <class T, int D, int BN, int NW, bool SPLIT, bool PRESCALE = true>
 void decode_kernel(const gr_attn_args& a, dim3 grid, hipStream_t st) {
   constexpr int LDS = gr_flash_lds<D, BN>::BYTES;
-  hipLaunchKernelGGL((gr_flash_fwd_kernel<T, D, BN, NW, 1, false, false, false, true, true, SPLIT>), grid,
+  hipLaunchKernelGGL((gr_flash_fwd_kernel<T, D, BN, NW, 1, false, false, false, true, true, SPLIT, PRESCALE>), grid,
                      dim3(NW * 64), LDS, st, a);
 }
 
@@ -177,9 +211,11 @@ int launch_decode(gr_attn_args a, int S, void* ws, size_t ws_bytes, bool fixed_w
                        a.scale_log2);
     return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_decode combine launch");
   }
-  const int nw = a.Nq <= 32 ? 1 : a.Nq <= 64 ? 2 : 4;
+  // fp16 with scale log2(e) > 1: Q as given (one wave per query tile, 32-key tiles)
+  const bool unscaled = gr_is_same<T, _Float16>::value && a.scale_log2 > 1.0f;
+  const int nw = unscaled ? 1 : a.Nq <= 32 ? 1 : a.Nq <= 64 ? 2 : 4;
   const long long nqt = (a.Nq + 32 * nw - 1) / (32 * nw);
-  const bool bn64 = a.N % 64 == 0;
+  const bool bn64 = !unscaled && a.N % 64 == 0;
   const int bn = bn64 ? 64 : 32;
   const int tiles = a.N / bn;
   if (S < 1) S = 1;
@@ -195,7 +231,12 @@ int launch_decode(gr_attn_args a, int S, void* ws, size_t ws_bytes, bool fixed_w
     a.part_ml = a.part_o + (size_t)S * a.B * a.H * a.Nq * D;
   }
   const dim3 grid((unsigned)nblk, (unsigned)S);
-  if (S > 1) {
+  if (unscaled) {
+    if constexpr (gr_is_same<T, _Float16>::value) {
+      if (S > 1) decode_kernel<T, D, 32, 1, true, false>(a, grid, st);
+      else decode_kernel<T, D, 32, 1, false, false>(a, grid, st);
+    }
+  } else if (S > 1) {
     if (bn64) decode_nw<T, D, 64, true>(a, nw, grid, st);
     else decode_nw<T, D, 32, true>(a, nw, grid, st);
   } else {
@@ -258,9 +299,10 @@ __global__ __launch_bounds__(256) void gr_flash32_merge_kernel(gr_attn_args a, c
 // demand. Calls on one stream run in order, so they can share it; a buffer
 // that grew is kept (queued work may still read it) until the process ends.
 // hipStreamPerThread names a different stream in every host thread, so its
-// buffers are kept per thread as well. Only problems of at most 256 query
-// blocks split, so a buffer stays below 256 * 32 rows * 8 parts * (D + 2)
-// floats (34 MiB at D = 128).
+// buffers are kept per thread as well (one per host thread that ever split
+// on it, none freed before the process ends). A split launch has at most
+// kF32SplitTarget workgroups of 32 query rows (query blocks x parts), so a
+// buffer stays below 256 * 32 * (D + 2) floats (4.3 MB at D = 128).
 struct F32Workspace {
   int dev;
   hipStream_t st;
@@ -373,10 +415,6 @@ int attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, i
       if (all[t][i] < 0 || (all[t][i] % 8) != 0)
         return gr::fail(GR_E_ARG, "gr_attn_fwd: strides must be non-negative multiples of 8 elements");
   if (!(scale > 0.f)) return gr::fail(GR_E_ARG, "gr_attn_fwd: scale must be positive");
-  // fp16 pre-scales Q by scale * log2(e) in fp16: above 1 a finite q could overflow
-  if (dtype == GR_F16 && scale * 1.4426950408889634f > 1.0f)
-    return gr::fail(GR_E_ARG, "gr_attn_fwd: fp16 needs scale * log2(e) <= 1 (scale <= 0.693; got %g); use bf16",
-                    (double)scale);
   gr_attn_args a;
   a.q = q;
   a.k = k;
@@ -396,6 +434,10 @@ int attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, i
   a.lse = lse;
   a.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = (hipStream_t)stream;
+  // fp16 pre-scales Q by scale * log2(e) in fp16; above 1 a finite q could
+  // overflow, so such calls take the kernels that keep Q as given
+  if (dtype == GR_F16 && a.scale_log2 > 1.0f)
+    return dispatch_unscaled_q(a, D, causal != 0, k_transposed != 0, block_m, block_n, st);
   if (dtype == GR_F16) return dispatch_shape<_Float16>(a, D, causal != 0, k_transposed != 0, block_m, block_n, st);
   if (dtype == GR_BF16) return dispatch_shape<__bf16>(a, D, causal != 0, k_transposed != 0, block_m, block_n, st);
   if (dtype == GR_F32) return attn_fwd_f32(a, D, causal != 0, k_transposed != 0, lse != nullptr, st);
@@ -449,10 +491,6 @@ int attn_decode(const char* who, const void* q, const void* k, const void* v, vo
       if (all[t][i] < 0 || (all[t][i] % 8) != 0)
         return gr::fail(GR_E_ARG, "%s: strides must be non-negative multiples of 8 elements", who);
   if (!(scale > 0.f)) return gr::fail(GR_E_ARG, "%s: scale must be positive", who);
-  // more than 4 queries run the flash body, which pre-scales Q in fp16 (see gr_attn_fwd)
-  if (dtype == GR_F16 && Nq > 4 && scale * 1.4426950408889634f > 1.0f)
-    return gr::fail(GR_E_ARG, "%s: fp16 with more than 4 queries needs scale * log2(e) <= 1 (got scale %g); use bf16",
-                    who, (double)scale);
   gr_attn_args a;
   a.q = q;
   a.k = k;

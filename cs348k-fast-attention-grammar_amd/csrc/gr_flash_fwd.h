@@ -349,8 +349,11 @@ __device__ __forceinline__ void gr_flash_qk_from(gr_f32x16 (&s)[BN / 32][QB], co
     }
 }
 
+// PRESCALE = false keeps fp16 Q as given and scales every score on the VALU
+// instead (as bf16 does): the launch path for fp16 with scale log2(e) > 1,
+// where the pre-scaled Q could overflow.
 template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT, bool PIPE, bool TR = false,
-          bool DIRECT = false, bool SPLIT = false>
+          bool DIRECT = false, bool SPLIT = false, bool PRESCALE = true>
 __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* lds) {
   typedef gr_mfma<T> MF;
   typedef typename MF::vec8 vec8;
@@ -422,7 +425,7 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
   // relative to the base and p = 2^s needs no VALU multiply-add per score. m
   // then holds the base in those units (scale log2(e) q.k). fp16 only: bf16
   // keeps Q as given.
-  constexpr bool CI = GR_FLASH_OPT && TR && gr_is_same<T, _Float16>::value;
+  constexpr bool CI = GR_FLASH_OPT && PRESCALE && TR && gr_is_same<T, _Float16>::value;
   gr_f32x16 cinit[QB];
   auto prescale_q = [&]() {
     if constexpr (CI) {
@@ -633,7 +636,7 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
           make_p(gr_ic<0>{}, z);
           bool bad = fresh || stale;
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb) bad |= !(lt[qb] <= 3.0e38f);   // an inf (or NaN) p
+          for (int qb = 0; qb < QB; ++qb) bad |= !(lt[qb] <= MF::PMAX);   // an overflowed p (or a NaN)
           ok = !gr_any(bad);
           // the next tile's K fragment reads first (their latency hides
           // behind the first exponentials), then per 32-key half block of
@@ -651,13 +654,20 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
         } else {
           gr_flash_qk_from<T, D, BN, QB, KTR>(s, ks0 + ODD * L::KS, qf, cinit, l32, g);
           mask();
-          if (!gr_any(fresh)) {
-            const float z[QB] = {};
-            make_p(gr_ic<0>{}, z);
-            bool bad = false;
+          // Also the first tile (m = -inf, scores relative to base 0) takes
+          // the fast path when its row sums show that base 0 works: no p past
+          // the P type's range, and a sum of at least 2^-6 over the lane's
+          // BN / 2 <= 64 keys, so that its largest p is >= 2^-12, a normal P.
+          const float z[QB] = {};
+          make_p(gr_ic<0>{}, z);
+          bool bad = false;
 #pragma unroll
-            for (int qb = 0; qb < QB; ++qb) bad |= !(lt[qb] <= 3.0e38f);   // an inf (or NaN) p
-            ok = !gr_any(bad);
+          for (int qb = 0; qb < QB; ++qb)
+            bad |= !(lt[qb] <= MF::PMAX) || (m[qb] == -GR_INF && !(lt[qb] >= 0x1p-6f));
+          ok = !gr_any(bad);
+          if (ok && fresh) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) if (m[qb] == -GR_INF) m[qb] = 0.f;
           }
         }
         if (!ok) {
@@ -733,20 +743,25 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) fresh |= m[qb] == -GR_INF;
         bool ok = false;
-        if (gr_any(fresh)) {
-          scores();
-        } else {
+        {
           // the scores and their exponentials in one block, so the first
-          // blocks' exponentials can run while the last score MFMAs do
+          // blocks' exponentials can run while the last score MFMAs do; the
+          // first tile (m = -inf) tries base 0 and keeps it when its row sums
+          // lie in [2^-6, the P type's range], as in the fp16 path
           scores();
           float nmc[QB];
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb) nmc[qb] = -m[qb] * c;
+          for (int qb = 0; qb < QB; ++qb) nmc[qb] = m[qb] == -GR_INF ? 0.f : -m[qb] * c;
           make_p(nmc);
           bool bad = false;
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb) bad |= !(lt[qb] <= 3.0e38f);   // an inf (or NaN) p
+          for (int qb = 0; qb < QB; ++qb)
+            bad |= !(lt[qb] <= MF::PMAX) || (m[qb] == -GR_INF && !(lt[qb] >= 0x1p-6f));
           ok = !gr_any(bad);
+          if (ok && gr_any(fresh)) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) if (m[qb] == -GR_INF) m[qb] = 0.f;
+          }
         }
         if (!ok) {
           float nmc[QB];
@@ -965,10 +980,10 @@ struct gr_flash_wpe {
 // Kernel wrapper used by the prebuilt library; the grammar renderer emits its
 // own wrappers with baked-in shapes around the same body.
 template <class T, int D, int BN, int NW, int QB, bool CAUSAL, bool KT_LAYOUT, bool PIPE, bool TR = false,
-          bool DIRECT = false, bool SPLIT = false>
+          bool DIRECT = false, bool SPLIT = false, bool PRESCALE = true>
 __global__ __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(gr_flash_wpe<D, BN, NW, QB, KT_LAYOUT, PIPE>::value)))
 void gr_flash_fwd_kernel(gr_attn_args a) {
   extern __shared__ __attribute__((aligned(16))) char gr_lds[];
-  gr_flash_fwd_body<T, D, BN, NW, QB, CAUSAL, KT_LAYOUT, PIPE, TR, DIRECT, SPLIT>(a, gr_lds);
+  gr_flash_fwd_body<T, D, BN, NW, QB, CAUSAL, KT_LAYOUT, PIPE, TR, DIRECT, SPLIT, PRESCALE>(a, gr_lds);
 }

@@ -228,6 +228,17 @@ def decode_splits(B: int, H: int, Nq: int, N: int, cu_count: int = 256) -> int:
     return max(1, min(want, N // 256 if N >= 256 else 1))
 
 
+def decode_splits_noalloc(B: int, H: int, Nq: int, N: int, D: int, cu_count: int = 256) -> int:
+    """decode_splits, lowered until the key parts' partials fit the library's
+    scratch array (rt.DECODE_SCRATCH_BYTES), which gr_attn_decode_noalloc
+    cannot grow. One part needs no scratch."""
+    L = rt.lib()
+    s = decode_splits(B, H, Nq, N, cu_count)
+    while s > 1 and int(L.gr_attn_decode_workspace(B, H, Nq, D, s)) > rt.DECODE_SCRATCH_BYTES:
+        s -= 1
+    return s
+
+
 def bind_flash_attention_decode(q, k, v, *, scale: float | None = None, splits: int = 0, out=None,
                                 workspace=None, stream=None):
     """Validate once and return (launch, out) for gr_attn_decode, arguments
@@ -275,7 +286,8 @@ def bind_flash_attention_decode_noalloc(q, k, v, *, scale: float | None = None, 
     key-split partials in the library's per-device scratch array, so neither
     the binding (given `out`) nor a launch allocates device memory. Launches
     that overlap on one device race on that array. Raises if the split needs
-    more than rt.DECODE_SCRATCH_BYTES."""
+    more than rt.DECODE_SCRATCH_BYTES; splits = 0 picks the largest split
+    decode_splits allows that fits it (decode_splits_noalloc)."""
     import torch
     for name, t in (("q", q), ("k", k), ("v", v)):
         if not t.is_cuda:
@@ -294,7 +306,7 @@ def bind_flash_attention_decode_noalloc(q, k, v, *, scale: float | None = None, 
         scale = 1.0 / math.sqrt(D)
     L = rt.lib()
     if splits <= 0:
-        splits = decode_splits(B, H, Nq, N, rt.device_info(q.device.index or 0)["cu_count"])
+        splits = decode_splits_noalloc(B, H, Nq, N, D, rt.device_info(q.device.index or 0)["cu_count"])
     fn = L.gr_attn_decode_noalloc
     args = (ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()),
             ctypes.c_void_p(out.data_ptr()), rt.dtype_code(q.dtype), B, H, Nq, N, D,

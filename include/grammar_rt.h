@@ -52,7 +52,7 @@ int gr_device_info(int device, long long* out5);
  *      grammar/kernel_ast.py:1228-1229) ------------------------------------ */
 
 /* Compile HIP C++ source `src` with hiprtc for gfx950. Options are passed
- * through (include paths, -D...). On success *code/*code_size receive a
+ * through (include paths, -D...). On success *code and *code_size receive a
  * malloc'd code object (free with gr_free_code). On a compile error the hiprtc
  * log is copied to `log` (truncated to loglen) and GR_E_COMPILE is returned.
  * Thread-safe: independent programs may be compiled concurrently. No HIP
@@ -107,17 +107,21 @@ int gr_plan_time(gr_plan* p, void* stream, int warmup, int iters, int mode, floa
  *  dtype: GR_F16 or GR_BF16 (fp32 accumulate). With GR_F16 the kernel
  *  rounds Q * scale * log2(e) to fp16 once (the scores then need no per-score
  *  scaling); that cannot overflow when scale * log2(e) <= 1 (as for the
- *  default 1/sqrt(D) with D >= 3), and a larger fp16 scale is refused with
- *  GR_E_ARG (bf16 takes any scale). GR_F32 (the reference's own dtype, fp32
+ *  default 1/sqrt(D) with D >= 3). A larger fp16 scale (e.g. 1 for a
+ *  pre-scaled q) takes kernels that keep Q as given and scale every score,
+ *  on one tile only: block_m 64, block_n 32 (0 / 0 pick it; N a multiple of
+ *  64). bf16 always keeps Q as given. GR_F32 (the reference's own dtype, fp32
  *  throughout on the fp32 matrix cores): non-causal only, N a multiple of 32,
  *  block_m and block_n ignored (a workgroup owns 32 queries and splits its
  *  keys over its waves); not for gr_attn_fwd_train. When B * H * N / 32 query
  *  blocks would leave CUs idle (N a multiple of 256, at most 128 blocks), the
  *  keys of a query block are also split over 2, 4 or 8 workgroups and a
  *  second launch merges their partials, which sit in a workspace the library
- *  allocates once per (device, stream) and grows on demand (a grown buffer is
- *  kept until the process ends; at most 34 MiB): call once on a stream
- *  before capturing such calls into a graph.
+ *  allocates once per (device, stream) and grows on demand: at most
+ *  256 * 32 * (D + 2) * 4 bytes (4.3 MB at D = 128), since a split launch has
+ *  at most 256 workgroups of 32 queries. A grown buffer is kept until the
+ *  process ends, and on the per-thread default stream each host thread keeps
+ *  its own. Call once on a stream before capturing such calls into a graph.
  *  Q, V, O: [B, H, N, D] with strides {batch, head, seq} in elements
  *  (unit stride along D). K: [B, H, N, D] if k_transposed == 0, else KT
  *  [B, H, D, N] whose k_strides = {batch, head, d} (unit stride along N).

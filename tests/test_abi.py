@@ -59,3 +59,20 @@ def test_null_arguments_are_rejected_without_a_device():
     rc = L.gr_attn_fwd(None, None, None, None, 1, 1, 1, 128, 64, rt._ll3(0, 0, 0), rt._ll3(0, 0, 0),
                        rt._ll3(0, 0, 0), rt._ll3(0, 0, 0), 0, 0, ctypes.c_float(0.125), 0, 0, None)
     assert rc == rt.GR_E_ARG and "null" in rt.last_error()
+
+
+def test_noalloc_default_split_fits_the_scratch_array():
+    """The split gr_attn_decode_noalloc is given by default never needs more
+    partials than the library's scratch array holds (host-side sizing only)."""
+    from grammar import runtime as rt
+    from grammar.attention import decode_splits, decode_splits_noalloc
+    L = rt.lib()
+    for B, H, Nq, N, D in ((1, 64, 128, 4096, 128), (1, 32, 64, 8192, 128), (2, 3, 1, 4096, 64),
+                           (4, 16, 1, 8192, 128), (8, 64, 4, 2048, 128)):
+        s = decode_splits_noalloc(B, H, Nq, N, D)
+        assert 1 <= s <= decode_splits(B, H, Nq, N)
+        assert s == 1 or int(L.gr_attn_decode_workspace(B, H, Nq, D, s)) <= rt.DECODE_SCRATCH_BYTES
+    # the shape the usual split would overflow: 8 parts need 34 MB, so it is lowered
+    assert decode_splits(1, 64, 128, 4096) == 8
+    assert int(L.gr_attn_decode_workspace(1, 64, 128, 128, 8)) > rt.DECODE_SCRATCH_BYTES
+    assert decode_splits_noalloc(1, 64, 128, 4096, 128) < 8

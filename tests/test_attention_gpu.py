@@ -275,8 +275,55 @@ def test_rejects_bad_shapes():
         from grammar.attention import flash_attention_fwd
         flash_attention_fwd(q.cpu(), q.cpu(), q.cpu())   # no CPU path
     q = torch.zeros(1, 1, 256, 64, dtype=torch.float16, device=dev)
-    with pytest.raises(rt.GrError, match="log2"):
-        _run(q, q, q, scale=1.0)             # fp16 Q pre-scale would exceed 1: refused, not overflowed
+    with pytest.raises(rt.GrError, match="64 x 32"):
+        _run(q, q, q, scale=1.0, block_m=256, block_n=128)   # scale log2(e) > 1 in fp16: one tile only
+
+
+@pytest.mark.parametrize("causal,kt", [(False, False), (True, True), (False, True)])
+def test_fp16_scale_above_one_keeps_q_as_given(causal, kt):
+    """fp16 with scale log2(e) > 1 (scale 1, a pre-scaled q): Q * scale log2(e)
+    could overflow fp16, so these calls keep Q as given and scale every score
+    (as torch SDPA accepts any scale). Includes entries of q that the fp16
+    pre-scale would have turned into inf."""
+    dev = _cuda()
+    g = torch.Generator("cpu").manual_seed(41)
+    B, H, N, D = 1, 2, 256, 64
+    q = (torch.randn((B, H, N, D), generator=g) / 8).half()
+    q[0, 0, 5, :4] = 60000.0 / 64           # q * log2(e) * 64 would pass fp16's 65504 if pre-scaled by 64
+    k = torch.randn((B, H, N, D), generator=g).half()
+    v = torch.randn((B, H, N, D), generator=g).half()
+    print(f"[case] fp16 scale 1.0 causal={causal} k_transposed={kt}", flush=True)
+    kk = k.transpose(-1, -2).contiguous() if kt else k
+    o = _run(q.to(dev), kk.to(dev), v.to(dev), scale=1.0, causal=causal, k_transposed=kt)
+    ref = O.attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), causal=causal, scale=1.0)
+    _check(o, ref, f"fp16 scale 1 causal={causal} kt={kt}")
+
+
+def test_fp16_scale_above_one_training_and_decode():
+    """The same path through the training forward (lse) and the decode
+    launch with more than four queries (the flash body), split and not."""
+    dev = _cuda()
+    from grammar.attention import flash_attention_decode, flash_attention_fwd_train
+    g = torch.Generator("cpu").manual_seed(42)
+    q = (torch.randn((1, 2, 128, 64), generator=g) / 8).half()
+    k = torch.randn((1, 2, 128, 64), generator=g).half()
+    v = torch.randn((1, 2, 128, 64), generator=g).half()
+    print("[case] fp16 scale 1.0 training forward", flush=True)
+    o, lse = flash_attention_fwd_train(q.to(dev), k.to(dev), v.to(dev), scale=1.0)
+    torch.cuda.synchronize()
+    ref = O.attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), scale=1.0)
+    _check(o, ref, "fp16 scale 1 training forward")
+    lref = O.attention_lse(q.float().numpy(), k.float().numpy(), scale=1.0)
+    assert np.abs(lse.cpu().numpy() - lref).max() <= 2e-3
+    kd = torch.randn((1, 2, 1024, 64), generator=g).half()
+    vd = torch.randn((1, 2, 1024, 64), generator=g).half()
+    qd = (torch.randn((1, 2, 40, 64), generator=g) / 8).half()
+    dref = O.attention(qd.float().numpy(), kd.float().numpy(), vd.float().numpy(), scale=1.0)
+    for splits in (1, 3):
+        print(f"[case] fp16 scale 1.0 decode Nq40 N1024 splits {splits}", flush=True)
+        od = flash_attention_decode(qd.to(dev), kd.to(dev), vd.to(dev), scale=1.0, splits=splits)
+        torch.cuda.synchronize()
+        _check(od, dref, f"fp16 scale 1 decode splits {splits}")
 
 
 DECODE = [

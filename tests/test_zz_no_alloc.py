@@ -120,3 +120,33 @@ def test_python_binding_uses_the_noalloc_entry():
     ref_launch()
     torch.cuda.synchronize()
     assert torch.equal(out, ref_out)
+
+
+def test_default_split_fits_the_scratch_array():
+    """splits = 0 picks the split for the scratch array: at B1 H64 Nq128 N4096
+    D128 the usual decode split (8 parts, 34 MB of partials) would not fit,
+    so the binding lowers it; the result equals gr_attn_decode at the same
+    split bit for bit, and the oracle on sampled heads."""
+    dev = _cuda()
+    from grammar import runtime as rt
+    from grammar.attention import bind_flash_attention_decode_noalloc, decode_splits, decode_splits_noalloc
+    B, H, Nq, N, D = 1, 64, 128, 4096, 128
+    cu = rt.device_info(0)["cu_count"]
+    s_noalloc = decode_splits_noalloc(B, H, Nq, N, D, cu)
+    L = rt.lib()
+    assert int(L.gr_attn_decode_workspace(B, H, Nq, D, s_noalloc)) <= rt.DECODE_SCRATCH_BYTES
+    print(f"[case] noalloc default split B{B} H{H} Nq{Nq} N{N} D{D}: decode_splits {decode_splits(B, H, Nq, N, cu)}, "
+          f"noalloc {s_noalloc}", flush=True)
+    q, k, v = (t.to(dev) for t in _inputs(B, H, Nq, N, D, torch.bfloat16, seed=5))
+    launch, got = bind_flash_attention_decode_noalloc(q, k, v)
+    launch()
+    want = torch.empty_like(q)
+    need = int(L.gr_attn_decode_workspace(B, H, Nq, D, s_noalloc))
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+    assert _call(False, q, k, v, want, s_noalloc, ws) == 0, rt.last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    for h in (0, 37, 63):
+        ref = O.attention(q[0, h].float().cpu().numpy(), k[0, h].float().cpu().numpy(), v[0, h].float().cpu().numpy())
+        mx, mn = O.errors(got[0, h].float().cpu().numpy(), ref)
+        assert np.isfinite(mx) and mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL, (h, mx, mn)
