@@ -4,7 +4,7 @@ fp16 MFMA peak on one MI355X at B=4, H=16, N=1024, d=64 (BASELINE.json
 config C2), with the descent's evals/min measured in the same run.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2|C3]
-                    [--search-seconds S] [--kernel descent|handwritten|fp32|PATH]
+                    [--search-seconds S] [--kernel descent|handwritten|fp32|hipblaslt-mlp|PATH]
 
 1. Descent: the stochastic rewrite descent runs from the naive 8-stage
    attention program (every stage its own kernel, full-extent tiles) for at
@@ -413,6 +413,27 @@ def run_descent(cfg, seconds: float, seed: int):
     return best, info
 
 
+def hipblaslt_mlp(steps: int, warmup: int, seed: int) -> dict:
+    """The library reference point for the C4 GEMMs: torch.matmul (hipBLASLt
+    on ROCm) on X W1 and H W2 at C4's shapes and inputs, plain GEMMs with no
+    epilogue, each timed like every other leg. It gives rocprofv3 a committed
+    command that runs hipBLASLt's kernels for these shapes."""
+    import torch
+    from grammar.workloads import C4, mlp_inputs
+    dev = torch.device("cuda:0")
+    x, w1, w2 = mlp_inputs(C4, seed=seed, device=dev)
+    h = torch.empty((C4.M, C4.Hd), dtype=x.dtype, device=dev)
+    y = torch.empty((C4.M, C4.Dm), dtype=x.dtype, device=dev)
+    flops = 2 * C4.M * C4.Dm * C4.Hd
+    ms1 = timed(lambda: torch.matmul(x, w1, out=h), steps, warmup)
+    ms2 = timed(lambda: torch.matmul(h, w2, out=y), steps, warmup)
+    log(f"[bench] hipBLASLt C4: X W1 {ms1:.4f} ms, H W2 {ms2:.4f} ms")
+    return {"metric": "C4 GEMM TFLOP/s, torch.matmul (hipBLASLt)", "steps": steps, "warmup": warmup,
+            "x_w1": {"ms": round(ms1, 6), "tflops": round(flops / (ms1 * 1e-3) / 1e12, 3)},
+            "h_w2": {"ms": round(ms2, 6), "tflops": round(flops / (ms2 * 1e-3) / 1e12, 3)},
+            "shapes": {"X": [C4.M, C4.Dm], "W1": [C4.Dm, C4.Hd], "W2": [C4.Hd, C4.Dm]}}
+
+
 def bench_module(path: str, steps: int, warmup: int, seed: int) -> dict:
     """Time one saved module -- a rendered .hip (it carries its launch plan
     and KERNEL_META) or a .json with a program key -- on seeded inputs,
@@ -422,15 +443,19 @@ def bench_module(path: str, steps: int, warmup: int, seed: int) -> dict:
     import torch
     from grammar.hip_module import HipModule
     from grammar.workloads import torch_dtype
+    causal = False
     if path.endswith(".json"):
-        from grammar.kernel_ast import emit_module, program_from_key
+        from grammar.kernel_ast import _iter_computes, emit_module, program_from_key
         with open(path) as f:
             saved = json.load(f)
-        src = emit_module(program_from_key(saved["key"], saved.get("dtype")))
+        prog = program_from_key(saved["key"], saved.get("dtype"))
+        causal = any(c.op == "causal" for loop in prog.body for c in _iter_computes(loop.body))
+        src = emit_module(prog)
     else:
         with open(path) as f:
             src = f.read()
     mod = HipModule(src)
+    causal = causal or any(st.get("tiles", {}).get("causal") for st in mod.plan["steps"])
     meta = mod.KERNEL_META
     g = torch.Generator("cpu").manual_seed(seed)
     dt = torch_dtype(mod.plan["dtype"])
@@ -459,7 +484,7 @@ def bench_module(path: str, steps: int, warmup: int, seed: int) -> dict:
     check = None
     if set(named) == {"Q", "KT", "V"}:
         import run_attention_search as RS
-        want = RS.attention_reference(1.0 / math.sqrt(named["Q"].shape[-1]))(named)
+        want = RS.attention_reference(1.0 / math.sqrt(named["Q"].shape[-1]), causal)(named)
     elif set(named) == {"X", "W1", "W2"}:
         import run_mlp_search as MS
         # build_mlp_ln's block ends in the normalised tensor "out", build_mlp_silu's in "y"
@@ -502,7 +527,8 @@ def main() -> int:
     ap.add_argument("--config", default="C2", choices=["C2", "C3"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--kernel", default="descent",
-                    help="descent | handwritten | fp32 (only the fp32 configs through gr_attn_fwd) | PATH of a "
+                    help="descent | handwritten | fp32 (only the fp32 configs through gr_attn_fwd) | hipblaslt-mlp "
+                         "(torch.matmul on the two C4 GEMMs, the library reference point) | PATH of a "
                          "saved module (.hip as RunLogger writes it, or a .json holding a program key): re-time "
                          "that module alone (reference bench.py --kernel)")
     ap.add_argument("--search-seconds", type=float, default=60.0, dest="search_seconds",
@@ -546,6 +572,9 @@ def main() -> int:
 
     if args.kernel == "fp32":
         print(json.dumps(fp32_attention(args.steps, args.seed)), flush=True)
+        return 0
+    if args.kernel == "hipblaslt-mlp":
+        print(json.dumps(hipblaslt_mlp(args.steps, args.warmup, args.seed)), flush=True)
         return 0
     if args.kernel not in ("descent", "handwritten"):
         print(json.dumps(bench_module(args.kernel, args.steps, args.warmup, args.seed)), flush=True)

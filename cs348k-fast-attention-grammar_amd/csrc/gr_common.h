@@ -46,9 +46,6 @@ template <> struct gr_mfma<_Float16> {
   typedef gr_f16x8 vec8;
   typedef gr_f16x4 vec4;
   typedef gr_f16x2 vec2;
-  // Largest finite value of the type: a tile's row sum of the rounded p at
-  // most this means none of them overflowed.
-  static constexpr float PMAX = 65504.0f;
   // acc + a.x + a.y, products exact, fp32 accumulate (v_dot2c_f32_f16).
   static __device__ __forceinline__ float sum2(vec2 a, float acc) {
     const vec2 one = {(_Float16)1.0f, (_Float16)1.0f};
@@ -66,7 +63,6 @@ template <> struct gr_mfma<__bf16> {
   typedef gr_bf16x8 vec8;
   typedef gr_bf16x4 vec4;
   typedef gr_bf16x2 vec2;
-  static constexpr float PMAX = 3.0e38f;
   static __device__ __forceinline__ float sum2(vec2 a, float acc) {
     const vec2 one = {(__bf16)1.0f, (__bf16)1.0f};
     return __builtin_amdgcn_fdot2_f32_bf16(a, one, acc, false);

@@ -636,7 +636,7 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
           make_p(gr_ic<0>{}, z);
           bool bad = fresh || stale;
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb) bad |= !(lt[qb] <= MF::PMAX);   // an overflowed p (or a NaN)
+          for (int qb = 0; qb < QB; ++qb) bad |= !(lt[qb] <= 3.0e38f);   // an inf (or NaN) p
           ok = !gr_any(bad);
           // the next tile's K fragment reads first (their latency hides
           // behind the first exponentials), then per 32-key half block of
@@ -654,20 +654,13 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
         } else {
           gr_flash_qk_from<T, D, BN, QB, KTR>(s, ks0 + ODD * L::KS, qf, cinit, l32, g);
           mask();
-          // Also the first tile (m = -inf, scores relative to base 0) takes
-          // the fast path when its row sums show that base 0 works: no p past
-          // the P type's range, and a sum of at least 2^-6 over the lane's
-          // BN / 2 <= 64 keys, so that its largest p is >= 2^-12, a normal P.
-          const float z[QB] = {};
-          make_p(gr_ic<0>{}, z);
-          bool bad = false;
+          if (!gr_any(fresh)) {
+            const float z[QB] = {};
+            make_p(gr_ic<0>{}, z);
+            bool bad = false;
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb)
-            bad |= !(lt[qb] <= MF::PMAX) || (m[qb] == -GR_INF && !(lt[qb] >= 0x1p-6f));
-          ok = !gr_any(bad);
-          if (ok && fresh) {
-#pragma unroll
-            for (int qb = 0; qb < QB; ++qb) if (m[qb] == -GR_INF) m[qb] = 0.f;
+            for (int qb = 0; qb < QB; ++qb) bad |= !(lt[qb] <= 3.0e38f);   // an inf (or NaN) p
+            ok = !gr_any(bad);
           }
         }
         if (!ok) {
@@ -743,25 +736,20 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) fresh |= m[qb] == -GR_INF;
         bool ok = false;
-        {
+        if (gr_any(fresh)) {
+          scores();
+        } else {
           // the scores and their exponentials in one block, so the first
-          // blocks' exponentials can run while the last score MFMAs do; the
-          // first tile (m = -inf) tries base 0 and keeps it when its row sums
-          // lie in [2^-6, the P type's range], as in the fp16 path
+          // blocks' exponentials can run while the last score MFMAs do
           scores();
           float nmc[QB];
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb) nmc[qb] = m[qb] == -GR_INF ? 0.f : -m[qb] * c;
+          for (int qb = 0; qb < QB; ++qb) nmc[qb] = -m[qb] * c;
           make_p(nmc);
           bool bad = false;
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb)
-            bad |= !(lt[qb] <= MF::PMAX) || (m[qb] == -GR_INF && !(lt[qb] >= 0x1p-6f));
+          for (int qb = 0; qb < QB; ++qb) bad |= !(lt[qb] <= 3.0e38f);   // an inf (or NaN) p
           ok = !gr_any(bad);
-          if (ok && gr_any(fresh)) {
-#pragma unroll
-            for (int qb = 0; qb < QB; ++qb) if (m[qb] == -GR_INF) m[qb] = 0.f;
-          }
         }
         if (!ok) {
           float nmc[QB];

@@ -397,7 +397,7 @@ void {kname}({params}) {{
     return code, {"kernel": kname, "grid": [grid, 1, 1], "block": [nt, 1, 1], "lds": lds,
                   "args": args, "lowering": "flash",
                   "tiles": {"block_m": f["BM"], "block_n": f["BN"], "waves": f["NW"], "qb": f["QB"],
-                            "pipe": f.get("pipe", 0)}}
+                            "pipe": f.get("pipe", 0), "causal": bool(f["causal"])}}
 
 
 # ---------------------------------------------------------------------------

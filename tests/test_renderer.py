@@ -85,7 +85,7 @@ def test_flash_lowering_selected_for_fp16_flash_structure():
     p = C.p_flash_attention(B=2, H=2, N=256, d=64, bm=128, bn=64, dtype="fp16")
     plan = parse_plan(emit_module(p))
     assert [s["lowering"] for s in plan["steps"]] == ["flash"]
-    assert plan["steps"][0]["tiles"] == {"block_m": 128, "block_n": 64, "waves": 4, "qb": 1, "pipe": 0}
+    assert plan["steps"][0]["tiles"] == {"block_m": 128, "block_n": 64, "waves": 4, "qb": 1, "pipe": 0, "causal": False}
     # the same structure in fp32: the fp32 flash kernel, keys split over waves
     # (block_n keys per wave), its partials in module-scope device arrays
     p32 = C.p_flash_attention(B=2, H=2, N=256, d=64, bm=64, bn=32, dtype="fp32")
@@ -127,7 +127,7 @@ def test_flash_schedule_knobs_reach_the_renderer_and_the_key():
     names["SCHED_O.qb"].set(2)
     assert p.body[0].knobs == {"pipe": 1, "qb": 2}
     tiles = parse_plan(emit_module(p))["steps"][0]["tiles"]
-    assert tiles == {"block_m": 256, "block_n": 64, "waves": 4, "qb": 2, "pipe": 1}
+    assert tiles == {"block_m": 256, "block_n": 64, "waves": 4, "qb": 2, "pipe": 1, "causal": False}
     assert "gr_flash_fwd_body<_Float16, 64, 64, 4, 2, false, true, true," in emit_module(p)
     key = structural_key(p)
     assert key != base_key and structural_key(program_from_key(key)) == key
