@@ -24,6 +24,20 @@ int launch_gemm(const gr_gemm_args& a, int batch, hipStream_t st) {
   return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_gemm launch");
 }
 
+// The 256 x 256 tile: four waves (one per SIMD) of 128 x 128, the
+// hand-ordered main loop of gr_gemm_w4_body.
+template <class T, bool KM, int EPI, int BK>
+int launch_gemm_w4(const gr_gemm_args& a, int batch, hipStream_t st) {
+  if (a.K % BK)
+    return gr::fail(GR_E_ARG, "gr_gemm: K=%d must be a multiple of the k tile %d", a.K, BK);
+  const long long nblk = (long long)((a.M + 255) / 256) * ((a.N + 255) / 256);
+  if (nblk <= 0 || nblk > 0x7fffffffLL || batch > 65535)
+    return gr::fail(GR_E_ARG, "gr_gemm: grid (%lld tiles, batch %d) out of range", nblk, batch);
+  hipLaunchKernelGGL((gr_gemm_w4_kernel<T, KM, EPI, BK>), dim3((unsigned)nblk, (unsigned)batch), dim3(256),
+                     gr_gemm_w4_lds<BK>::value, st, a);
+  return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_gemm launch");
+}
+
 // (block_m, block_n) -> (k tile, wave grid) compiled into the library; the
 // 128x128 and 256x256 tiles take 64-deep k tiles when K allows, else 32.
 template <class T, bool KM, int EPI>
@@ -37,8 +51,7 @@ int dispatch_tile(const gr_gemm_args& a, int batch, int bm, int bn, hipStream_t 
   if (bm == 256 && bn == 128) return launch_gemm<T, 256, 128, 32, 2, 2, KM, EPI>(a, batch, st);
   if (bm == 128 && bn == 256) return launch_gemm<T, 128, 256, 32, 2, 2, KM, EPI>(a, batch, st);
   if (bm == 256 && bn == 256)
-    return k64 ? launch_gemm<T, 256, 256, 64, 2, 4, KM, EPI>(a, batch, st)
-               : launch_gemm<T, 256, 256, 32, 2, 4, KM, EPI>(a, batch, st);
+    return k64 ? launch_gemm_w4<T, KM, EPI, 64>(a, batch, st) : launch_gemm_w4<T, KM, EPI, 32>(a, batch, st);
   return gr::fail(GR_E_ARG, "gr_gemm: unsupported tile (block_m=%d, block_n=%d)", bm, bn);
 }
 

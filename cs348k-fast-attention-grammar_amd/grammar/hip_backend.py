@@ -89,7 +89,7 @@ FLASH_BM = {32: (1, 1), 64: (2, 1), 128: (4, 1), 256: (8, 1)}   # block_m -> def
 # softmax.
 FLASH_KNOBS = {"qb": (1, 2), "pipe": (0, 1)}
 FLASH_KNOB_DEFAULTS = {"qb": 1, "pipe": 0}     # what an absent knob means
-KNOB_DEFAULTS = {**FLASH_KNOB_DEFAULTS, "ksplit": 1}
+KNOB_DEFAULTS = {**FLASH_KNOB_DEFAULTS, "ksplit": 1, "waves": 4}
 
 
 FLASH_DEFAULT_BN = {64: 128, 128: 64}    # key tile when the stage does not tile the key axis
@@ -293,13 +293,15 @@ def template_tilings(loop: ParallelLoop, program: Program) -> list:
 def schedule_knobs(loop: ParallelLoop, program: Program) -> dict:
     """The schedule knobs the renderer honours for this stage, each with its
     choices and current value: {name: (choices, current)}: the flash kernel's
-    query blocks per wave and pipelined schedule, the fp32 GEMM's split K;
-    empty for other stages."""
+    query blocks per wave and pipelined schedule, the fp32 GEMM's split K,
+    the 16-bit 256 x 256 GEMM's waves; empty for other stages."""
     f = _match_flash(loop, program)
     if f is None:
         gm = _match_gemm(loop, program)
         if gm is not None and gm.get("f32"):
             return {"ksplit": (GEMM_KSPLIT, gm["ksplit"])}
+        if gm is not None and gm.get("w4_ok"):
+            return {"waves": (GEMM_TILE_WAVES, gm["waves"])}
         return {}
     if f.get("f32"):
         return {}
@@ -412,6 +414,11 @@ GEMM_KSPLIT = (1, 2, 4, 8)
 GEMM_WS_LIMIT = 32 << 20
 GEMM_WAVES_M = {32: 1, 64: 1, 128: 2, 256: 2}
 GEMM_WAVES_N = {32: 1, 64: 1, 128: 2, 256: 2}
+# 16-bit 256 x 256 tiles with 32- or 64-deep k tiles (schedule knob "waves"):
+# 4 = one wave per SIMD, 128 x 128 each, the hand-ordered main loop of
+# gr_gemm_w4_body (the default); 8 = two waves per SIMD, 128 x 64 each
+# (gr_gemm_body)
+GEMM_TILE_WAVES = (4, 8)
 
 
 def _gemm_lds(bm, bn, bk):
@@ -564,10 +571,15 @@ def _match_gemm(loop: ParallelLoop, program: Program):
     if M * K % 8 or K * N % 8 or K % 8 or N % 8:
         return None
     wgm, wgn = _gemm_waves(BM, BN)
+    w4_ok = BM == 256 and BN == 256 and BK in (32, 64)
+    waves = int((getattr(loop, "knobs", None) or {}).get("waves", KNOB_DEFAULTS["waves"]))
+    if waves not in GEMM_TILE_WAVES:
+        waves = KNOB_DEFAULTS["waves"]
     return {"a": aload.source, "b": bload.source, "c": loop.out, "M": M, "N": N, "K": K, "batch": batch,
             "a_sb": M * K if a_batched else 0, "b_sb": K * N if b_batched else 0, "c_sb": M * N,
             "kmajor": kmajor, "act": act, "alpha": alpha, "BM": BM, "BN": BN, "BK": BK, "WGM": wgm, "WGN": wgn,
-            "res": res.source if res is not None else None}
+            "res": res.source if res is not None else None,
+            "w4_ok": w4_ok, "waves": waves, "W4": w4_ok and waves == 4}
 
 
 def _render_gemm_f32_split(loop, program, f, args, params, km) -> tuple:
@@ -671,6 +683,27 @@ void {kname}({params}) {{
         return code, {"kernel": kname, "grid": [grid, f["batch"], 1], "block": [nt, 1, 1],
                       "lds": _gemm_f32_lds(f["BM"], f["BN"], f["BK"], f["kmajor"]), "args": args,
                       "lowering": "gemm", "tiles": {"block_m": f["BM"], "block_n": f["BN"], "block_k": f["BK"]}}
+    if f.get("W4"):
+        code = f"""
+// stage {loop.out}: MFMA GEMM {f['M']}x{f['N']}x{f['K']} (x{f['batch']}), tile 256x256x{f['BK']},
+// four waves of 128 x 128 (one per SIMD, hand-ordered main loop)
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
+void {kname}({params}) {{
+  extern __shared__ __attribute__((aligned(16))) char gr_gemm_smem[];
+  gr_gemm_args a;
+  a.a = {_cname(f['a'])}; a.b = {_cname(f['b'])}; a.c = {_cname(f['c'])};
+  a.a_sb = {f['a_sb']}LL; a.a_sm = {f['K']};
+  a.b_sb = {f['b_sb']}LL; a.b_s = {f['K'] if f['kmajor'] else f['N']};
+  a.c_sb = {f['c_sb']}LL; a.c_sm = {f['N']};
+  a.M = {f['M']}; a.N = {f['N']}; a.K = {f['K']};
+  a.alpha = {_flt(f['alpha'])};{res_line}
+  gr_gemm_w4_body<{T}, {km}, {f['act']}, {f['BK']}>(a, gr_gemm_smem);
+}}
+"""
+        grid = -(-f["M"] // 256) * -(-f["N"] // 256)
+        return code, {"kernel": kname, "grid": [grid, f["batch"], 1], "block": [256, 1, 1],
+                      "lds": _gemm_lds(256, 256, f["BK"]), "args": args, "lowering": "gemm",
+                      "tiles": {"block_m": 256, "block_n": 256, "block_k": f["BK"], "waves": 4}}
     tpl = f"{T}, {f['BM']}, {f['BN']}, {f['BK']}, {f['WGM']}, {f['WGN']}, {km}, {f['act']}"
     nt = f["WGM"] * f["WGN"] * 64
     code = f"""

@@ -218,8 +218,9 @@ int gr_attn_decode_noalloc(const void* q, const void* k, const void* v, void* o,
  *  epilogue: GR_EPI_NONE, GR_EPI_RELU or GR_EPI_SILU, applied to alpha*acc.
  *  (block_m, block_n) in {(128,128), (256,128), (128,256), (256,256)}
  *  (0 = 256). Any M; N a multiple of 8; K a multiple of 32 (the square
- *  tiles use 64-deep k tiles when K allows). Edge tiles of C are stored
- *  only where valid. */
+ *  tiles use 64-deep k tiles when K allows). The 256 x 256 tile runs four
+ *  waves of 128 x 128 (one per SIMD); the other tiles run eight waves.
+ *  Edge tiles of C are stored only where valid. */
 #define GR_EPI_NONE 0
 #define GR_EPI_RELU 1
 #define GR_EPI_SILU 2

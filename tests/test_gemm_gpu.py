@@ -58,6 +58,11 @@ CASES = [
     (2, 72, 40, 64, "bf16", "relu", 1.0, True, (256, 256)),
     (1, 1000, 264, 160, "fp16", "none", 0.5, True, (128, 256)),
     (1, 33, 8, 32, "bf16", "silu", 1.0, False, (256, 128)),
+    # the 256 x 256 tile's one-wave body: one k tile, three 32-deep tiles (only
+    # the loop's tail runs), bf16 with a [K, N] B, a batch with a K-major B
+    (1, 256, 256, 64, "bf16", "none", 1.0, False, (256, 256)),
+    (1, 512, 512, 96, "fp16", "silu", 1.0, False, (256, 256)),
+    (2, 256, 512, 192, "bf16", "relu", 0.5, True, (256, 256)),
 ]
 
 

@@ -186,6 +186,38 @@ def test_residual_add_lowers_to_the_gemm_epilogue():
         assert "a.r = t_X; a.r_sb = 131072LL; a.r_sm = 512;" in src and body in src, dt
 
 
+def test_gemm_waves_knob():
+    """16-bit GEMM stages with 256 x 256 tiles offer the schedule knob waves:
+    4 (the default, kept as an absent knob) renders the one-wave-per-SIMD body
+    with its hand-ordered main loop, 8 the two-waves-per-SIMD body. Smaller
+    tiles and fp32 programs offer no such knob."""
+    import run_mlp_search as RM
+    from grammar import rewrites as R
+    from grammar.hip_backend import schedule_knobs
+    from grammar.kernel_ast import structural_key
+    p = RM.build_mlp_silu(512, 256, 512, tile=256, dtype="fp16")
+    p = R.merge(p, p.body[0], p.body[1])
+    assert [schedule_knobs(s, p) for s in p.body] == [{"waves": ((4, 8), 4)}] * 2
+    key0, src0 = structural_key(p), emit_module(p)
+    steps = parse_plan(src0)["steps"]
+    assert [s["block"] for s in steps] == [[256, 1, 1]] * 2 and [s["lds"] for s in steps] == [131072] * 2
+    assert [s["tiles"]["waves"] for s in steps] == [4, 4]
+    assert "gr_gemm_w4_body<_Float16, false, 2, 64>(a, gr_gemm_smem);" in src0      # SiLU epilogue
+    assert "gr_gemm_w4_body<_Float16, false, 0, 64>(a, gr_gemm_smem);" in src0
+    p.body[1].knobs["waves"] = 8
+    assert structural_key(p) != key0
+    src8 = emit_module(p)
+    assert "gr_gemm_body<_Float16, 256, 256, 64, 2, 4, false, 0>(a, gr_gemm_smem);" in src8
+    assert parse_plan(src8)["steps"][1]["block"] == [512, 1, 1]
+    p.body[1].knobs.pop("waves")
+    assert structural_key(p) == key0 and emit_module(p) == src0
+    q = RM.build_mlp_silu(512, 256, 512, tile=128, dtype="fp16")
+    q = R.merge(q, q.body[0], q.body[1])
+    assert [schedule_knobs(s, q) for s in q.body] == [{}, {}]
+    f = RM.build_mlp_ln(256, 512, 1024, tile=64)
+    assert "waves" not in schedule_knobs(f.body[2], f)
+
+
 def test_fp32_gemm_split_k_knob():
     """fp32 GEMM stages offer the schedule knob ksplit: the K loop split over
     workgroups (grid z), the partials in a module-scope workspace, and a

@@ -322,6 +322,49 @@ def test_residual_add_fuses_into_the_gemm(dt):
         assert np.isfinite(got).all() and err <= tol * max(1.0, float(np.max(np.abs(want[name]))))
 
 
+@pytest.mark.parametrize("dt", ["fp16", "bf16"])
+def test_gemm_waves_knob_schedules_agree(dt):
+    """The LN block's two GEMM stages (a = relu(X @ W1), r = a @ W2 + X) at
+    256 x 256 tiles under both values of the schedule knob waves: the
+    one-wave-per-SIMD body (4, the default) and the two-waves-per-SIMD body
+    (8) accumulate every output in the same k order, so r and out agree bit
+    for bit; both against the tile interpreter on the same rounded inputs."""
+    _cuda()
+    import run_mlp_search as RM
+    from grammar import rewrites as R
+    from grammar.hip_module import load_module
+    M, Dm, H = 512, 256, 512
+    p = RM.build_mlp_ln(M, Dm, H, tile=256, dtype=dt)
+    p = R.merge(p, p.body[2], p.body[3])
+    p = R.merge(p, p.body[0], p.body[1])
+    ins = {k: v.float().cpu().numpy() for k, v in RM.mlp_inputs(M, Dm, H, dt, seed=5).items()}
+    rnd = (lambda x: np.asarray(x, dtype=np.float16).astype(np.float32)) if dt == "fp16" else \
+        (lambda x: torch.from_numpy(np.asarray(x, dtype=np.float32)).bfloat16().float().numpy())
+    want = run_program(p, ins, storage_round=rnd)
+    tol = 2e-2 if dt == "bf16" else 5e-3
+    runs = {}
+    for waves in (4, 8):
+        for st in p.body[:2]:
+            st.knobs.pop("waves", None)
+            if waves != 4:
+                st.knobs["waves"] = waves
+        mod = load_module(emit_module(p))
+        gemm_steps = [s for s in mod.plan["steps"] if s["lowering"] == "gemm"]
+        assert [s["block"][0] for s in gemm_steps] == [256 if waves == 4 else 512] * 2
+        print(f"[case] LN block {dt} M={M} Dm={Dm} H={H} waves={waves}", flush=True)
+        args = [torch.from_numpy(ins[n]).to(_cuda()).to(mod.dtype) for n in mod.inputs]
+        tensors = mod.run_with(args)
+        torch.cuda.synchronize()
+        runs[waves] = {n: tensors[n].float().cpu().numpy() for n in ("r", "out")}
+        for name in ("r", "out"):
+            got = runs[waves][name]
+            err = float(np.max(np.abs(got - want[name])))
+            print(f"[waves] {dt} waves={waves} {name}: max|d| {err:.2e}", flush=True)
+            assert np.isfinite(got).all() and err <= tol * max(1.0, float(np.max(np.abs(want[name]))))
+    for name in ("r", "out"):
+        assert np.array_equal(runs[4][name], runs[8][name]), name
+
+
 @pytest.mark.parametrize("ks_a,ks_r", [(2, 4), (8, 8), (4, 1)])
 def test_fp32_split_k_gemm_stages(ks_a, ks_r):
     """fp32 GEMM stages with K split over workgroups (schedule knob ksplit):
