@@ -86,9 +86,11 @@ FLASH_BM = {32: (1, 1), 64: (2, 1), 128: (4, 1), 256: (8, 1)}   # block_m -> def
 # block_m / (32 qb) waves; 2 halves the LDS fragment reads per MFMA at twice
 # the registers, head dim 64 only) and "pipe" the software-pipelined
 # schedule that issues the next key tile's score MFMAs during this tile's
-# softmax.
-FLASH_KNOBS = {"qb": (1, 2), "pipe": (0, 1)}
-FLASH_KNOB_DEFAULTS = {"qb": 1, "pipe": 0}     # what an absent knob means
+# softmax; "w2" the two-waves-per-SIMD body with the hand-ordered main loop
+# (gr_flash_w2.h: fp16, head dim 64, non-causal, 256 x 64 tiles, N a multiple
+# of 256, scale log2(e) <= 1), on by default where it applies.
+FLASH_KNOBS = {"qb": (1, 2), "pipe": (0, 1), "w2": (0, 1)}
+FLASH_KNOB_DEFAULTS = {"qb": 1, "pipe": 0, "w2": 1}     # what an absent knob means
 KNOB_DEFAULTS = {**FLASH_KNOB_DEFAULTS, "ksplit": 1, "waves": 4}
 
 
@@ -232,9 +234,14 @@ def _match_flash(loop: ParallelLoop, program: Program):
     pipe = 1 if int(knobs.get("pipe", 0)) else 0
     if D == 128 and qb > 1:
         return None
+    w2_ok = program.dtype == "fp16" and D == 64 and not causal and BM == 256 and BN == 64 and \
+        N % 256 == 0 and scale * LOG2E <= 1.0
+    w2 = w2_ok and bool(int(knobs.get("w2", FLASH_KNOB_DEFAULTS["w2"])))
+    if w2:
+        qb, nw, pipe = 1, 8, 0
     return {"q": qload.source, "kt": ktload.source, "v": vload.source, "o": loop.out,
             "lead": _prod(qs[:nb]), "N": N, "D": D, "BM": BM, "BN": BN, "NW": nw, "QB": qb,
-            "pipe": pipe, "causal": causal, "scale": scale}
+            "pipe": pipe, "causal": causal, "scale": scale, "w2_ok": w2_ok, "W2": w2}
 
 
 def _match_flash32(loop, rl, tile, nb, N, D, causal, scale, qload, ktload, vload, lead):
@@ -294,7 +301,9 @@ def schedule_knobs(loop: ParallelLoop, program: Program) -> dict:
     """The schedule knobs the renderer honours for this stage, each with its
     choices and current value: {name: (choices, current)}: the flash kernel's
     query blocks per wave and pipelined schedule, the fp32 GEMM's split K,
-    the 16-bit 256 x 256 GEMM's waves; empty for other stages."""
+    the 16-bit 256 x 256 GEMM's waves, the flash body with two waves per SIMD
+    (which, when on, is the only flash knob offered: the other two do not
+    apply to it); empty for other stages."""
     f = _match_flash(loop, program)
     if f is None:
         gm = _match_gemm(loop, program)
@@ -305,9 +314,13 @@ def schedule_knobs(loop: ParallelLoop, program: Program) -> dict:
         return {}
     if f.get("f32"):
         return {}
+    if f.get("W2"):
+        return {"w2": (FLASH_KNOBS["w2"], 1)}
     out = {"pipe": (FLASH_KNOBS["pipe"], f["pipe"])}
     if f["D"] == 64:
         out["qb"] = (FLASH_KNOBS["qb"], f["QB"])
+    if f.get("w2_ok"):
+        out["w2"] = (FLASH_KNOBS["w2"], 0)
     return out
 
 
@@ -371,6 +384,8 @@ def _render_flash(loop, program, f) -> tuple:
     args = _loop_tensors(loop)
     params = ", ".join(f"{'const ' if a != loop.out else ''}{T}* __restrict__ {_cname(a)}" for a in args)
     N, D = f["N"], f["D"]
+    if f.get("W2"):
+        return _render_flash_w2(loop, program, f, kname, args, params)
     pipe = "true" if f.get("pipe") else "false"
     nt = f["NW"] * 64
     # K^T / V tiles straight into LDS when each thread moves whole 16-byte chunks
@@ -400,6 +415,40 @@ void {kname}({params}) {{
                   "args": args, "lowering": "flash",
                   "tiles": {"block_m": f["BM"], "block_n": f["BN"], "waves": f["NW"], "qb": f["QB"],
                             "pipe": f.get("pipe", 0), "causal": bool(f["causal"])}}
+
+
+def _render_flash_w2(loop, program, f, kname, args, params) -> tuple:
+    """A flash stage on gr_flash_w2_body: 256 queries per workgroup as 8 waves
+    of 32 (two per SIMD), 64-key tiles in two 8-slot LDS rings (160 KiB of LDS
+    with the per-wave Q / O areas)."""
+    N, D = f["N"], f["D"]
+    code = f"""
+// stage {loop.out}: flash attention, two waves per SIMD with a hand-ordered main loop
+// (256 queries/workgroup as 8 waves of 32, 64-key tiles)
+extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
+void {kname}({params}) {{
+  extern __shared__ __attribute__((aligned(16))) char gr_flash_smem[];
+  gr_attn_args a;
+  a.q = {_cname(f['q'])}; a.k = {_cname(f['kt'])}; a.v = {_cname(f['v'])}; a.o = {_cname(f['o'])};
+  a.q_sb = {N * D}LL; a.q_sh = 0; a.q_sn = {D};
+  a.k_sb = {N * D}LL; a.k_sh = 0; a.k_sn = {N};
+  a.v_sb = {N * D}LL; a.v_sh = 0; a.v_sn = {D};
+  a.o_sb = {N * D}LL; a.o_sh = 0; a.o_sn = {D};
+  a.B = {f['lead']}; a.H = 1; a.N = {N}; a.Nq = {N};
+  a.kchunk = {N}; a.part_o = nullptr; a.part_ml = nullptr;
+  a.scale_log2 = {_flt(f['scale'] * LOG2E)};
+  gr_flash_w2_body<true>(a, gr_flash_smem);
+}}
+"""
+    grid = f["lead"] * (N // 256)
+    return code, {"kernel": kname, "grid": [grid, 1, 1], "block": [512, 1, 1], "lds": FLASH_W2_LDS,
+                  "args": args, "lowering": "flash",
+                  "tiles": {"block_m": 256, "block_n": 64, "waves": 8, "qb": 1, "pipe": 0,
+                            "causal": False, "w2": 1}}
+
+
+# GR_FLASH_W2_LDS: K and V rings of 8 tiles of 8 KiB, 4 KiB of Q / O per wave
+FLASH_W2_LDS = 2 * 8 * 64 * 64 * 2 + 8 * 32 * 64 * 2
 
 
 # ---------------------------------------------------------------------------
@@ -1614,6 +1663,8 @@ def render_module(program: Program, fn_name: str = "fn", check: bool = False) ->
         parts.insert(0, "#define GR_FLASH_OPT 0  // a flash stage's scale * log2(e) exceeds 1: no fp16 Q pre-scale")
     if any(f.get("f32") for f in flash):
         parts.insert(parts.index('#include "gr_gemm_f32.h"') + 1, '#include "gr_flash_f32.h"')
+    if any(f.get("W2") for f in flash):
+        parts.insert(parts.index('#include "gr_gemm_f32.h"') + 1, '#include "gr_flash_w2.h"')
     steps = []
     over, excess = [], 0
     matched = []

@@ -83,6 +83,14 @@ SMALL = [
     (1, 2, 512, 128, "fp16", True, True, 129, 32),
     (1, 2, 512, 128, "bf16", False, True, 257, 64),
     (1, 1, 128, 64, "fp16", False, False, 129, 128),
+    # fp16 d 64 non-causal 256 x 64: the two-waves-per-SIMD body (gr_flash_w2.h),
+    # from the fewest tiles (4) to 36 and 40 tiles (three and seven steps after
+    # the groups of eight)
+    (1, 2, 256, 64, "fp16", False, False, 256, 64),
+    (1, 2, 512, 64, "fp16", False, True, 256, 64),
+    (2, 3, 1024, 64, "fp16", False, False, 256, 64),
+    (1, 2, 2304, 64, "fp16", False, True, 256, 64),
+    (1, 1, 2560, 64, "fp16", False, False, 256, 64),
 ]
 
 
@@ -137,6 +145,26 @@ def test_c2_full_parity_and_layout_invariance():
     assert torch.equal(_run(qs, ks, vs), o)
     # Deterministic across launches.
     assert torch.equal(_run(qd, kd, vd), o)
+
+
+def test_c2_two_wave_body_layouts_and_strides():
+    """The two-waves-per-SIMD body (fp16, d 64, non-causal, 256 x 64 tiles;
+    gr_flash_w2.h) at the C2 shape: parity with the oracle; the K^T layout and
+    strided [B, N, H, D] views give the bitwise same output (the same operands
+    reach the same MFMAs); deterministic across launches."""
+    dev = _cuda()
+    from grammar.workloads import C2, attention_inputs
+    q, k, v = attention_inputs(C2, seed=0)
+    ref = O.attention(q.float().numpy(), k.float().numpy(), v.float().numpy())
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    kw = dict(block_m=256, block_n=64)
+    o = _run(qd, kd, vd, **kw)
+    _check(o, ref, "C2 two-wave body")
+    assert torch.equal(_run(qd, kd.transpose(-1, -2).contiguous(), vd, k_transposed=True, **kw), o)
+    qs, ks, vs = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (qd, kd, vd))
+    assert qs.stride() != qd.stride()
+    assert torch.equal(_run(qs, ks, vs, **kw), o)
+    assert torch.equal(_run(qd, kd, vd, **kw), o)
 
 
 def test_c2_key_permutation_property():

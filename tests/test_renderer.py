@@ -112,20 +112,34 @@ def test_flash_lowering_selected_for_fp16_flash_structure():
 
 
 def test_flash_schedule_knobs_reach_the_renderer_and_the_key():
-    """The flash stage's schedule knobs (query blocks per wave, software
-    pipelining) are descent parameters: they change the rendered kernel and
-    the structural key, survive program_from_key, and the renderer's default
-    is stored as an absent knob."""
+    """The flash stage's schedule knobs (the two-waves-per-SIMD body, query
+    blocks per wave, software pipelining) are descent parameters: they change
+    the rendered kernel and the structural key, survive program_from_key, and
+    the renderer's default is stored as an absent knob."""
     from grammar import optimization as O
     from grammar.kernel_ast import program_from_key, structural_key
     p = C.p_flash_attention(B=2, H=2, N=512, d=64, bm=256, bn=64, dtype="fp16")
     names = {q.name: q for q in O.parameter_vector(p)}
-    assert {"SCHED_O.qb", "SCHED_O.pipe"} <= set(names)
+    # fp16, d 64, non-causal, 256 x 64: the two-wave body is on by default and
+    # is then the only flash knob
+    assert [n for n in names if n.startswith("SCHED_")] == ["SCHED_O.w2"] and names["SCHED_O.w2"].current == 1
+    src = emit_module(p)
+    assert "gr_flash_w2_body<true>(a, gr_flash_smem);" in src and '#include "gr_flash_w2.h"' in src
+    st = parse_plan(src)["steps"][0]
+    assert st["block"] == [512, 1, 1] and st["lds"] == 163840 and st["grid"] == [4 * 2, 1, 1]
+    assert st["tiles"] == {"block_m": 256, "block_n": 64, "waves": 8, "qb": 1, "pipe": 0, "causal": False, "w2": 1}
+    w2_key, w2_src = structural_key(p), src
+    names["SCHED_O.w2"].set(0)
+    assert p.body[0].knobs == {"w2": 0} and structural_key(p) != w2_key
+    assert "gr_flash_w2" not in emit_module(p)
+    names = {q.name: q for q in O.parameter_vector(p)}
+    assert {"SCHED_O.qb", "SCHED_O.pipe", "SCHED_O.w2"} <= set(names)
     assert names["SCHED_O.qb"].ladder() == [1, 2] and names["SCHED_O.pipe"].current == 0
+    assert names["SCHED_O.w2"].current == 0
     base_key, base_src = structural_key(p), emit_module(p)
     names["SCHED_O.pipe"].set(1)
     names["SCHED_O.qb"].set(2)
-    assert p.body[0].knobs == {"pipe": 1, "qb": 2}
+    assert p.body[0].knobs == {"w2": 0, "pipe": 1, "qb": 2}
     tiles = parse_plan(emit_module(p))["steps"][0]["tiles"]
     assert tiles == {"block_m": 256, "block_n": 64, "waves": 4, "qb": 2, "pipe": 1, "causal": False}
     assert "gr_flash_fwd_body<_Float16, 64, 64, 4, 2, false, true, true," in emit_module(p)
@@ -133,7 +147,16 @@ def test_flash_schedule_knobs_reach_the_renderer_and_the_key():
     assert key != base_key and structural_key(program_from_key(key)) == key
     names["SCHED_O.pipe"].set(0)
     names["SCHED_O.qb"].set(1)
-    assert p.body[0].knobs == {} and structural_key(p) == base_key and emit_module(p) == base_src
+    assert p.body[0].knobs == {"w2": 0} and structural_key(p) == base_key and emit_module(p) == base_src
+    names["SCHED_O.w2"].set(1)
+    assert p.body[0].knobs == {} and structural_key(p) == w2_key and emit_module(p) == w2_src
+    # the two-wave body does not apply to other shapes: bf16, causal, other tiles
+    for q in (C.p_flash_attention(B=1, H=2, N=512, d=64, bm=256, bn=64, dtype="bf16"),
+              C.p_flash_attention(B=1, H=2, N=512, d=64, bm=256, bn=64, causal=True, dtype="fp16"),
+              C.p_flash_attention(B=1, H=2, N=512, d=64, bm=256, bn=128, dtype="fp16"),
+              C.p_flash_attention(B=1, H=2, N=512, d=64, bm=128, bn=64, dtype="fp16"),
+              C.p_flash_attention(B=1, H=2, N=512, d=64, bm=256, bn=64, scale=1.0, dtype="fp16")):
+        assert "SCHED_O.w2" not in {x.name for x in O.parameter_vector(q)} and "gr_flash_w2" not in emit_module(q)
     # head dim 128 offers no second query block per wave
     p128 = C.p_flash_attention(B=1, H=2, N=256, d=128, bm=128, bn=64, dtype="bf16")
     assert [q.name for q in O.parameter_vector(p128) if q.name.startswith("SCHED_")] == ["SCHED_O.pipe"]

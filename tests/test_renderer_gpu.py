@@ -83,12 +83,17 @@ FLASH = [
     (1, 2, 256, 64, 32, 128, False, "fp16"),
     # schedule knobs (descent parameters SCHED_O.pipe / SCHED_O.qb)
     (1, 4, 512, 64, 256, 128, False, "fp16", {"pipe": 1}),
-    (1, 4, 512, 64, 256, 64, False, "fp16", {"qb": 2}),
+    (1, 4, 512, 64, 256, 64, False, "fp16", {"qb": 2, "w2": 0}),
     (1, 4, 512, 64, 256, 64, True, "bf16", {"qb": 2, "pipe": 1}),
     (1, 2, 256, 128, 128, 64, True, "bf16", {"pipe": 1}),
     (2, 2, 256, 64, 128, 128, False, "bf16", {"qb": 2}),
     # scale 1 in fp16: no Q pre-scale (scale * log2(e) > 1)
     (1, 2, 256, 64, 128, 64, True, "fp16", {}, 1.0),
+    # fp16 d 64 non-causal 256 x 64: the two-waves-per-SIMD body (knob w2, on
+    # by default); 40 tiles leave seven steps after the groups of eight
+    (1, 4, 512, 64, 256, 64, False, "fp16"),
+    (2, 2, 1024, 64, 256, 64, False, "fp16", {"w2": 1}),
+    (1, 2, 2560, 64, 256, 64, False, "fp16"),
 ]
 
 
@@ -106,7 +111,11 @@ def test_flash_lowered_program_parity(case):
     mod = load_module(emit_module(prog))
     assert [s["lowering"] for s in mod.plan["steps"]] == ["flash"]
     tiles = mod.plan["steps"][0]["tiles"]
-    assert tiles["qb"] == knobs.get("qb", 1) and tiles["pipe"] == knobs.get("pipe", 0)
+    w2 = dt == "fp16" and d == 64 and not causal and (bm, bn) == (256, 64) and N % 256 == 0 and \
+        scale * 1.4426950408889634 <= 1.0 and knobs.get("w2", 1) == 1
+    assert tiles.get("w2", 0) == int(w2)
+    if not w2:
+        assert tiles["qb"] == knobs.get("qb", 1) and tiles["pipe"] == knobs.get("pipe", 0)
     q, kt, v = attention_inputs(AttnConfig("t", B, H, N, d, dt, causal), seed=3, k_transposed=True)
     o = mod.fn(kt.to(dev), q.to(dev), v.to(dev))          # sorted input names: KT, Q, V
     torch.cuda.synchronize()
