@@ -24,9 +24,11 @@
 // per-lane base plus an immediate: the step loop is unrolled over the ring's
 // eight slots so that every slot offset is a constant.
 //
-// Against gr_flash_fwd_body's 256 x 128 tile on one box: B4 H16 N4096 d64
-// 251 us against 272 us, B4 H16 N1024 (the C2 shape) level at ~20.5 us, where
-// the per-workgroup start and end weigh more.
+// Against gr_flash_fwd_body's 256 x 128 tile, interleaved on one box: B4 H16
+// N1024 d64 (the C2 shape) 17.45 us against 19.1-19.4 us, B1 H16 N4096 61.0 us
+// against 66.6 us. A straight-line fit over 7 to 63 steps per workgroup gives
+// 0.91 us per 64-key step (0.99) and 3.9 us per workgroup (4.1): the first Q
+// and tile loads, the O store and the launch.
 //
 // Softmax in exponent units, as the fp16 path of gr_flash_fwd_body: Q is
 // pre-scaled by scale log2(e) and the score MFMAs start from -base, so
@@ -99,10 +101,30 @@ __device__ __forceinline__ void gr_flash_w2_body(const gr_attn_args& a, char* ld
   // slot, chunk and half; with the step loop unrolled over the ring, every
   // slot index is a compile-time constant.
   constexpr int VOFF = NSLOT * TILE_K, QOFF = 2 * NSLOT * TILE_K;
+  // A tile is one direct load of K and one of V per thread, from a wave-uniform
+  // (scalar) tile base plus the lane's constant byte offset, so that moving to
+  // the next tile costs scalar arithmetic only; M0 (the LDS destination) is
+  // saved and restored once for both.
+  static_assert(KL::PER == 1 && VL::PER == 1 && KL::CHUNKS == NT && VL::CHUNKS == NT, "one chunk per thread");
+  const unsigned kgo = (unsigned)kl.goff[0] * 2u, vgo = (unsigned)vl.goff[0] * 2u;
+  const unsigned lbase = gr_lds_addr(lds) + kl.lwave;
   auto load_tile = [&](int t, int slot) {
     if (t < ntile) {
-      kl.load(Kp + t * k_tile, lds + slot * TILE_K);
-      vl.load(Vp + t * v_tile, lds + VOFF + slot * TILE_K);
+      const T* kb = Kp + t * k_tile;
+      const T* vb = Vp + t * v_tile;
+      unsigned saved;
+      asm volatile(
+          "s_mov_b32 %0, m0\n\t"
+          "s_mov_b32 m0, %3\n\t"
+          "s_nop 0\n\t"
+          "global_load_lds_dwordx4 %2, %1\n\t"
+          "s_mov_b32 m0, %6\n\t"
+          "s_nop 0\n\t"
+          "global_load_lds_dwordx4 %5, %4\n\t"
+          "s_mov_b32 m0, %0"
+          : "=&s"(saved)
+          : "s"(kb), "v"(kgo), "s"(lbase + slot * TILE_K), "s"(vb), "v"(vgo), "s"(lbase + VOFF + slot * TILE_K)
+          : "memory");
     }
   };
   // lane base of two transposing reads (gr_tr_frag) of a tile with 128-byte
