@@ -106,8 +106,14 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   const int nkb = a.N / BN;
-  const int logical = gr_xcd_remap((int)blockIdx.x, (int)gridDim.x);
-  const int bh = logical / nkb, kb = logical % nkb;
+  int bh, kb;                                   // causal: key block 0 has the most queries
+  if constexpr (CAUSAL) {
+    gr_causal_order((int)blockIdx.x, (int)gridDim.x, nkb, bh, kb);
+  } else {
+    const int logical = gr_xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    bh = logical / nkb;
+    kb = logical % nkb;
+  }
   const long long base = (bh / a.H) * a.sb + (bh % a.H) * a.sh;
   const T* Q = static_cast<const T*>(a.q) + base;
   const T* K = static_cast<const T*>(a.k) + base;
@@ -268,10 +274,15 @@ void gr_attn_bwd_dq_kernel(gr_attn_bwd_args a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   const int nqt = a.N / BM;
-  const int logical = gr_xcd_remap((int)blockIdx.x, (int)gridDim.x);
-  const int bh = logical / nqt;
-  int qt = logical % nqt;
-  if (CAUSAL) qt = nqt - 1 - qt;              // the longest query tiles first
+  int bh, qt;
+  if constexpr (CAUSAL) {
+    gr_causal_order((int)blockIdx.x, (int)gridDim.x, nqt, bh, qt);
+    qt = nqt - 1 - qt;                        // the longest query tiles first
+  } else {
+    const int logical = gr_xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    bh = logical / nqt;
+    qt = logical % nqt;
+  }
   const long long base = (bh / a.H) * a.sb + (bh % a.H) * a.sh;
   const T* Q = static_cast<const T*>(a.q) + base;
   const T* K = static_cast<const T*>(a.k) + base;

@@ -371,10 +371,15 @@ __device__ __forceinline__ void gr_flash_fwd_body(const gr_attn_args& a, char* l
   const int g = lane >> 5, l32 = lane & 31;
   const int Nq = a.Nq;
   const int nqt = (Nq + BM - 1) / BM;
-  const int logical = gr_xcd_remap((int)blockIdx.x, (int)gridDim.x);
-  const int bh = logical / nqt;
-  int qt = logical % nqt;
-  if (CAUSAL) qt = nqt - 1 - qt;
+  int bh, qt;
+  if constexpr (CAUSAL) {
+    gr_causal_order((int)blockIdx.x, (int)gridDim.x, nqt, bh, qt);
+    qt = nqt - 1 - qt;                        // the longest query tiles first
+  } else {
+    const int logical = gr_xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    bh = logical / nqt;
+    qt = logical % nqt;
+  }
   const int b = bh / a.H, h = bh % a.H;
 
   // this workgroup's keys: all of them, or (SPLIT) part blockIdx.y
