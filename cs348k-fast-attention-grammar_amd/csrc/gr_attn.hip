@@ -10,6 +10,7 @@
 #include "gr_flash_decode.h"
 #include "gr_flash_f32.h"
 #include "gr_flash_w2.h"
+#include "gr_flash_w2h.h"
 #include "gr_host.h"
 #include "grammar_rt.h"
 
@@ -42,6 +43,17 @@ int launch_w2(const gr_attn_args& a, hipStream_t st) {
   return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_fwd launch");
 }
 
+// fp16 or bf16, D = 128, K transposed, causal or not, 256 x 64 tiles without
+// the training forward's log-sum-exp: two waves per SIMD with the
+// hand-ordered main loop (gr_flash_w2h.h); N a multiple of 256.
+template <class T, bool CAUSAL>
+int launch_w2h(const gr_attn_args& a, hipStream_t st) {
+  const long long nblk = (long long)a.B * a.H * (a.N / 256);
+  if (nblk <= 0 || nblk > 0x7fffffffLL) return gr::fail(GR_E_ARG, "gr_attn_fwd: grid size %lld out of range", nblk);
+  hipLaunchKernelGGL((gr_flash_w2h_kernel<T, CAUSAL>), dim3((unsigned)nblk), dim3(512), GR_FLASH_W2H_LDS, st, a);
+  return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_fwd launch");
+}
+
 // Tile configurations compiled into the library: (block_m, block_n) ->
 // (waves, query blocks per wave, key tile). One wave per 32 queries.
 // block_m 0 / block_n 0 pick the largest tiles that divide N (256 x 128 at
@@ -52,6 +64,8 @@ int dispatch_tiles(const gr_attn_args& a, int bm, int bn, hipStream_t st) {
   if (bn == 0) bn = (D == 64 && a.N % 128 == 0) ? 128 : a.N % 64 == 0 ? 64 : 32;
   if constexpr (gr_is_same<T, _Float16>::value && D == 64 && !CAUSAL)
     if (bm == 256 && bn == 64 && a.lse == nullptr && a.N % 256 == 0) return launch_w2<KT>(a, st);
+  if constexpr (D == 128 && KT)
+    if (bm == 256 && bn == 64 && a.lse == nullptr && a.N % 256 == 0 && a.Nq == a.N) return launch_w2h<T, CAUSAL>(a, st);
   if (bm == 256 && bn == 64) return launch_flash<T, D, 64, 8, 1, CAUSAL, KT>(a, st);
   if (bm == 256 && bn == 32) return launch_flash<T, D, 32, 8, 1, CAUSAL, KT>(a, st);
   if (bm == 128 && bn == 64) return launch_flash<T, D, 64, 4, 1, CAUSAL, KT>(a, st);

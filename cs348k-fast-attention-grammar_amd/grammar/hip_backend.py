@@ -87,8 +87,9 @@ FLASH_BM = {32: (1, 1), 64: (2, 1), 128: (4, 1), 256: (8, 1)}   # block_m -> def
 # the registers, head dim 64 only) and "pipe" the software-pipelined
 # schedule that issues the next key tile's score MFMAs during this tile's
 # softmax; "w2" the two-waves-per-SIMD body with the hand-ordered main loop
-# (gr_flash_w2.h: fp16, head dim 64, non-causal, 256 x 64 tiles, N a multiple
-# of 256, scale log2(e) <= 1), on by default where it applies.
+# (256 x 64 tiles, N a multiple of 256: gr_flash_w2.h for fp16, head dim 64,
+# non-causal, scale log2(e) <= 1; gr_flash_w2h.h for fp16 or bf16, head dim
+# 128, causal or not), on by default where it applies.
 FLASH_KNOBS = {"qb": (1, 2), "pipe": (0, 1), "w2": (0, 1)}
 FLASH_KNOB_DEFAULTS = {"qb": 1, "pipe": 0, "w2": 1}     # what an absent knob means
 KNOB_DEFAULTS = {**FLASH_KNOB_DEFAULTS, "ksplit": 1, "waves": 4}
@@ -234,8 +235,9 @@ def _match_flash(loop: ParallelLoop, program: Program):
     pipe = 1 if int(knobs.get("pipe", 0)) else 0
     if D == 128 and qb > 1:
         return None
-    w2_ok = program.dtype == "fp16" and D == 64 and not causal and BM == 256 and BN == 64 and \
-        N % 256 == 0 and scale * LOG2E <= 1.0
+    w2_ok = BM == 256 and BN == 64 and N % 256 == 0 and (
+        (program.dtype == "fp16" and D == 64 and not causal and scale * LOG2E <= 1.0) or
+        (program.dtype in ("fp16", "bf16") and D == 128))
     w2 = w2_ok and bool(int(knobs.get("w2", FLASH_KNOB_DEFAULTS["w2"])))
     if w2:
         qb, nw, pipe = 1, 8, 0
@@ -418,10 +420,17 @@ void {kname}({params}) {{
 
 
 def _render_flash_w2(loop, program, f, kname, args, params) -> tuple:
-    """A flash stage on gr_flash_w2_body: 256 queries per workgroup as 8 waves
-    of 32 (two per SIMD), 64-key tiles in two 8-slot LDS rings (160 KiB of LDS
-    with the per-wave Q / O areas)."""
+    """A flash stage on a two-waves-per-SIMD body: 256 queries per workgroup as
+    8 waves of 32, 64-key tiles; at head dim 64 gr_flash_w2_body (two 8-slot
+    LDS rings with per-wave Q / O areas), at 128 gr_flash_w2h_body (two 5-slot
+    rings, Q and O staged through them); 160 KiB of LDS either way."""
     N, D = f["N"], f["D"]
+    if D == 128:
+        body = f"gr_flash_w2h_body<{CTYPE[program.dtype]}, {'true' if f['causal'] else 'false'}>(a, gr_flash_smem);"
+        lds = FLASH_W2H_LDS
+    else:
+        body = "gr_flash_w2_body<true>(a, gr_flash_smem);"
+        lds = FLASH_W2_LDS
     code = f"""
 // stage {loop.out}: flash attention, two waves per SIMD with a hand-ordered main loop
 // (256 queries/workgroup as 8 waves of 32, 64-key tiles)
@@ -437,18 +446,20 @@ void {kname}({params}) {{
   a.B = {f['lead']}; a.H = 1; a.N = {N}; a.Nq = {N};
   a.kchunk = {N}; a.part_o = nullptr; a.part_ml = nullptr;
   a.scale_log2 = {_flt(f['scale'] * LOG2E)};
-  gr_flash_w2_body<true>(a, gr_flash_smem);
+  {body}
 }}
 """
     grid = f["lead"] * (N // 256)
-    return code, {"kernel": kname, "grid": [grid, 1, 1], "block": [512, 1, 1], "lds": FLASH_W2_LDS,
+    return code, {"kernel": kname, "grid": [grid, 1, 1], "block": [512, 1, 1], "lds": lds,
                   "args": args, "lowering": "flash",
                   "tiles": {"block_m": 256, "block_n": 64, "waves": 8, "qb": 1, "pipe": 0,
-                            "causal": False, "w2": 1}}
+                            "causal": bool(f["causal"]), "w2": 1}}
 
 
 # GR_FLASH_W2_LDS: K and V rings of 8 tiles of 8 KiB, 4 KiB of Q / O per wave
 FLASH_W2_LDS = 2 * 8 * 64 * 64 * 2 + 8 * 32 * 64 * 2
+# GR_FLASH_W2H_LDS: K^T and V rings of 5 tiles of 16 KiB
+FLASH_W2H_LDS = 2 * 5 * 64 * 128 * 2
 
 
 # ---------------------------------------------------------------------------
@@ -1663,8 +1674,10 @@ def render_module(program: Program, fn_name: str = "fn", check: bool = False) ->
         parts.insert(0, "#define GR_FLASH_OPT 0  // a flash stage's scale * log2(e) exceeds 1: no fp16 Q pre-scale")
     if any(f.get("f32") for f in flash):
         parts.insert(parts.index('#include "gr_gemm_f32.h"') + 1, '#include "gr_flash_f32.h"')
-    if any(f.get("W2") for f in flash):
+    if any(f.get("W2") and f["D"] == 64 for f in flash):
         parts.insert(parts.index('#include "gr_gemm_f32.h"') + 1, '#include "gr_flash_w2.h"')
+    if any(f.get("W2") and f["D"] == 128 for f in flash):
+        parts.insert(parts.index('#include "gr_gemm_f32.h"') + 1, '#include "gr_flash_w2h.h"')
     steps = []
     over, excess = [], 0
     matched = []

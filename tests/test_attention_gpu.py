@@ -91,6 +91,16 @@ SMALL = [
     (2, 3, 1024, 64, "fp16", False, False, 256, 64),
     (1, 2, 2304, 64, "fp16", False, True, 256, 64),
     (1, 1, 2560, 64, "fp16", False, False, 256, 64),
+    # d 128, K^T, 256 x 64: the d = 128 two-wave body (gr_flash_w2h.h), causal
+    # (the diagonal block alone at N 256) or not; 6 heads take the grid-wide
+    # causal order, 8 the per-XCD one
+    (1, 2, 256, 128, "bf16", True, True, 256, 64),
+    (1, 2, 256, 128, "fp16", False, True, 256, 64),
+    (1, 2, 512, 128, "bf16", True, True, 256, 64),
+    (2, 3, 1024, 128, "fp16", True, True, 256, 64),
+    (1, 8, 1024, 128, "bf16", True, True, 256, 64),
+    (1, 2, 2304, 128, "bf16", False, True, 256, 64),
+    (1, 1, 1280, 128, "fp16", True, True, 0, 0),
 ]
 
 
@@ -164,6 +174,52 @@ def test_c2_two_wave_body_layouts_and_strides():
     qs, ks, vs = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (qd, kd, vd))
     assert qs.stride() != qd.stride()
     assert torch.equal(_run(qs, ks, vs, **kw), o)
+    assert torch.equal(_run(qd, kd, vd, **kw), o)
+
+
+def test_d128_two_wave_body_rescales_a_growing_row_max():
+    """The d = 128 two-wave body takes its softmax base from the first tile it
+    visits (for causal, the diagonal block) and moves it only when a step's
+    row sum leaves the P type's range. Keys past the first 256 scaled up make
+    later scores far larger: by 12 (p up to about 2^40, past fp16's 2^16) in
+    fp16, by 40 (past fp32's 2^128, so the row sum overflows) in bf16, where V
+    is halved to keep the bf16 rounding of p and of O inside the bar. The
+    rescaling path runs in both; parity with the oracle."""
+    dev = _cuda()
+    from grammar.workloads import AttnConfig, attention_inputs
+    for dt, causal, grow in (("fp16", False, 12.0), ("fp16", True, 12.0), ("bf16", False, 40.0), ("bf16", True, 40.0)):
+        q, kt, v = attention_inputs(AttnConfig("t", 1, 2, 1024, 128, dt, causal), seed=7, k_transposed=True)
+        kt = kt.clone()
+        kt[..., 256:] = (kt[..., 256:].float() * grow).to(kt.dtype)
+        if dt == "bf16":
+            v = (v.float() * 0.5).to(v.dtype)
+        ref = O.attention(q.float().numpy(), kt.float().numpy(), v.float().numpy(), causal=causal, k_transposed=True)
+        o = _run(q.to(dev), kt.to(dev), v.to(dev), causal=causal, k_transposed=True, block_m=256, block_n=64)
+        _check(o, ref, f"d128 two-wave growing max {dt} causal={causal} x{grow:g}")
+
+
+def test_c3_two_wave_body_kt_full_size():
+    """C3 (B2 H32 N4096 d128 bf16 causal) with K given transposed, as the
+    grammar's programs hand it over: the d = 128 two-wave body. Finite, inside
+    each head's V hull, row 0 equal to V row 0, the oracle on sampled heads,
+    strided views bitwise equal, deterministic."""
+    dev = _cuda()
+    from grammar.workloads import C3, attention_inputs
+    q, kt, v = attention_inputs(C3, seed=0, k_transposed=True)
+    qd, kd, vd = q.to(dev), kt.to(dev), v.to(dev)
+    kw = dict(causal=True, k_transposed=True, block_m=256, block_n=64)
+    o = _run(qd, kd, vd, **kw)
+    of = o.float().cpu()
+    assert torch.isfinite(of).all()
+    vf = v.float()
+    assert bool(((of >= vf.amin(dim=2, keepdim=True) - 1e-2) & (of <= vf.amax(dim=2, keepdim=True) + 1e-2)).all())
+    assert (of[:, :, 0] - vf[:, :, 0]).abs().max().item() <= 1e-2
+    for b, h in ((0, 0), (1, 31), (0, 17)):
+        ref = O.attention(q[b, h].float().numpy(), kt[b, h].float().numpy(), v[b, h].float().numpy(), causal=True,
+                          k_transposed=True)
+        _check(of[b, h], ref, f"C3 K^T head ({b},{h})")
+    qs, vs = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (qd, vd))
+    assert torch.equal(_run(qs, kd, vs, **kw), o)
     assert torch.equal(_run(qd, kd, vd, **kw), o)
 
 

@@ -165,6 +165,33 @@ def test_flash_schedule_knobs_reach_the_renderer_and_the_key():
     assert sched == ["SCHED_S.ksplit", "SCHED_O.ksplit"], sched
 
 
+def test_flash_head_dim_128_two_wave_body():
+    """Head dim 128 at 256 x 64 tiles (fp16 or bf16, causal or not, N a
+    multiple of 256) renders the d = 128 two-waves-per-SIMD body
+    (gr_flash_w2h.h), on by default and then the only flash knob; off, the
+    stage falls back to the flash body with its pipelining knob."""
+    from grammar import optimization as O
+    for dt, ctype, causal in (("bf16", "__bf16", True), ("fp16", "_Float16", False), ("bf16", "__bf16", False)):
+        p = C.p_flash_attention(B=2, H=2, N=512, d=128, bm=256, bn=64, causal=causal, dtype=dt)
+        names = {q.name: q for q in O.parameter_vector(p)}
+        assert [n for n in names if n.startswith("SCHED_")] == ["SCHED_O.w2"] and names["SCHED_O.w2"].current == 1
+        src = emit_module(p)
+        assert f"gr_flash_w2h_body<{ctype}, {'true' if causal else 'false'}>(a, gr_flash_smem);" in src
+        assert '#include "gr_flash_w2h.h"' in src and '#include "gr_flash_w2.h"' not in src
+        st = parse_plan(src)["steps"][0]
+        assert st["block"] == [512, 1, 1] and st["lds"] == 163840 and st["grid"] == [4 * 2, 1, 1]
+        assert st["tiles"] == {"block_m": 256, "block_n": 64, "waves": 8, "qb": 1, "pipe": 0, "causal": causal,
+                               "w2": 1}
+        names["SCHED_O.w2"].set(0)
+        assert "gr_flash_w2h" not in emit_module(p) and parse_plan(emit_module(p))["steps"][0]["block"] == [512, 1, 1]
+        names = {q.name: q for q in O.parameter_vector(p)}
+        assert {"SCHED_O.pipe", "SCHED_O.w2"} == {n for n in names if n.startswith("SCHED_")}
+    # other tiles keep the flash body
+    for q in (C.p_flash_attention(B=1, H=2, N=512, d=128, bm=128, bn=64, causal=True, dtype="bf16"),
+              C.p_flash_attention(B=1, H=2, N=512, d=128, bm=256, bn=32, dtype="bf16")):
+        assert "SCHED_O.w2" not in {x.name for x in O.parameter_vector(q)} and "gr_flash_w2h" not in emit_module(q)
+
+
 def test_fp16_flash_with_large_scale_skips_the_q_prescale():
     """The fp16 flash kernel rounds Q * scale * log2(e) to fp16; a module whose
     flash stage has scale * log2(e) > 1 turns that off (GR_FLASH_OPT 0)."""

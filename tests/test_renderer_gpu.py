@@ -94,6 +94,13 @@ FLASH = [
     (1, 4, 512, 64, 256, 64, False, "fp16"),
     (2, 2, 1024, 64, 256, 64, False, "fp16", {"w2": 1}),
     (1, 2, 2560, 64, 256, 64, False, "fp16"),
+    # head dim 128 at 256 x 64: the d = 128 two-wave body (gr_flash_w2h.h),
+    # causal or not; off (w2 0), the flash body
+    (1, 2, 256, 128, 256, 64, True, "bf16"),
+    (2, 4, 1024, 128, 256, 64, True, "bf16"),
+    (1, 2, 512, 128, 256, 64, False, "fp16"),
+    (1, 2, 768, 128, 256, 64, True, "fp16"),
+    (1, 2, 512, 128, 256, 64, True, "bf16", {"w2": 0}),
 ]
 
 
@@ -111,8 +118,8 @@ def test_flash_lowered_program_parity(case):
     mod = load_module(emit_module(prog))
     assert [s["lowering"] for s in mod.plan["steps"]] == ["flash"]
     tiles = mod.plan["steps"][0]["tiles"]
-    w2 = dt == "fp16" and d == 64 and not causal and (bm, bn) == (256, 64) and N % 256 == 0 and \
-        scale * 1.4426950408889634 <= 1.0 and knobs.get("w2", 1) == 1
+    w2 = (bm, bn) == (256, 64) and N % 256 == 0 and knobs.get("w2", 1) == 1 and (
+        (dt == "fp16" and d == 64 and not causal and scale * 1.4426950408889634 <= 1.0) or d == 128)
     assert tiles.get("w2", 0) == int(w2)
     if not w2:
         assert tiles["qb"] == knobs.get("qb", 1) and tiles["pipe"] == knobs.get("pipe", 0)
