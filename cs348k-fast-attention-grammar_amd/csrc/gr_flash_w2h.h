@@ -192,8 +192,10 @@ __device__ __forceinline__ void gr_flash_w2h_body(const gr_attn_args& a, char* l
   auto vfrag = [&](int slot, int cc, int db) -> vec8 { return tr2(vbase[db] + slot * TILE + cc * 16 * (D * 2), gr_ic<D * 2>{}); };
 
   // Prologue: each wave's 32 Q rows into 8 KiB of ring slots 3 and 4 (before
-  // tiles 3 and 4 fill them), tiles 0, 1 and 2; all landed, Q into registers,
-  // then (after every wave has read its Q) tile 3.
+  // tiles 3 and 4 fill them), tiles 0, 1 and 2. Once Q and tile 0 have
+  // landed, Q goes into registers and tile 0's scores are computed while
+  // tiles 1 and 2 are still in flight; tile 3 is loaded once tile 1 has
+  // landed and every wave has read its Q.
   char* const qstage = lds + (wave < 4 ? 3 * TILE + wave * 8192 : VOFF + 3 * TILE + (wave - 4) * 8192);
   {
     gr_lds_loader<T, 32, D, 64> ql;
@@ -203,13 +205,11 @@ __device__ __forceinline__ void gr_flash_w2h_body(const gr_attn_args& a, char* l
   load_tile(0);
   load_tile(1);
   load_tile(2);
-  gr_wait_vmcnt<0>();
+  gr_wait_vmcnt<2 * PER_TILE>();                  // Q and tile 0 (every tile exists: ntile >= 4)
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   vec8 qf[8];
 #pragma unroll
   for (int ds = 0; ds < 8; ++ds) qf[ds] = gr_as<vec8>(gr_ld16(qstage + l32 * (D * 2) + gr_swz<D / 8>(l32, 2 * ds + g) * 16));
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  load_tile(3);
 
   // a score's key offset within its tile (perm32 order): element r of half kb
   // is key 32 kb + 16 (r / 8) + 8 g + r % 8; the lane's query is qw + l32
@@ -254,6 +254,10 @@ __device__ __forceinline__ void gr_flash_w2h_body(const gr_attn_args& a, char* l
         }
     lsum = l;
   }
+  // tile 1 landed, and every wave has read its Q (slots 3 and 4 are free)
+  gr_wait_vmcnt<PER_TILE>();
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  load_tile(3);
   // tile 1's scores (unscaled, from zero)
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
