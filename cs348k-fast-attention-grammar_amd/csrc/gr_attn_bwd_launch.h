@@ -9,6 +9,13 @@
 
 namespace {
 
+// fp16 with scale log2(e) <= 1: the kernels' pre-scaled forms (PRE), whose
+// scores come out of the MFMAs in log2 units relative to the row's L.
+template <class T>
+bool bwd_prescale(const gr_attn_bwd_args& a) {
+  return gr_is_same<T, _Float16>::value && a.scale * 1.4426950408889634f <= 1.0f;
+}
+
 // Backward tiles. dK/dV: (queries per tile, keys per workgroup) = (64, 128),
 // one wave per 32 keys. dQ: key tiles of 64, 8 waves (256 queries) per
 // workgroup when N allows it, else 4.
@@ -17,8 +24,15 @@ void launch_bwd_dq(const gr_attn_bwd_args& a, bool causal, hipStream_t st) {
   constexpr int DQ_BN = 64;
   const dim3 grid((unsigned)((long long)a.B * a.H * (a.N / (NW * 32))));
   constexpr int LDS = gr_attn_bwd_dq_lds<D, DQ_BN>::BYTES;
-  if (causal) hipLaunchKernelGGL((gr_attn_bwd_dq_kernel<T, D, NW, DQ_BN, true>), grid, dim3(NW * 64), LDS, st, a);
-  else hipLaunchKernelGGL((gr_attn_bwd_dq_kernel<T, D, NW, DQ_BN, false>), grid, dim3(NW * 64), LDS, st, a);
+  const bool pre = bwd_prescale<T>(a);
+  if (causal && pre)
+    hipLaunchKernelGGL((gr_attn_bwd_dq_kernel<T, D, NW, DQ_BN, true, true>), grid, dim3(NW * 64), LDS, st, a);
+  else if (causal)
+    hipLaunchKernelGGL((gr_attn_bwd_dq_kernel<T, D, NW, DQ_BN, true, false>), grid, dim3(NW * 64), LDS, st, a);
+  else if (pre)
+    hipLaunchKernelGGL((gr_attn_bwd_dq_kernel<T, D, NW, DQ_BN, false, true>), grid, dim3(NW * 64), LDS, st, a);
+  else
+    hipLaunchKernelGGL((gr_attn_bwd_dq_kernel<T, D, NW, DQ_BN, false, false>), grid, dim3(NW * 64), LDS, st, a);
 }
 
 template <class T, int D, int BM, int BN>
@@ -32,8 +46,13 @@ int launch_bwd(const gr_attn_bwd_args& a, bool causal, hipStream_t st) {
   if (rc) return rc;
   const dim3 grid((unsigned)((long long)a.B * a.H * (a.N / BN)));
   constexpr int LDS = gr_attn_bwd_lds<D, BM, BN>::BYTES;
-  if (causal) hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, true>), grid, dim3(BN / 32 * 64), LDS, st, a);
-  else hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, false>), grid, dim3(BN / 32 * 64), LDS, st, a);
+  constexpr bool CAN_PRE = !gr_attn_bwd_lds<D, BM, BN>::KV_LDS;   // K in registers
+  const bool pre = CAN_PRE && bwd_prescale<T>(a);
+  const dim3 blk(BN / 32 * 64);
+  if (causal && pre) hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, true, CAN_PRE>), grid, blk, LDS, st, a);
+  else if (causal) hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, true, false>), grid, blk, LDS, st, a);
+  else if (pre) hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, false, CAN_PRE>), grid, blk, LDS, st, a);
+  else hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, false, false>), grid, blk, LDS, st, a);
   return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd dK/dV launch");
 }
 

@@ -91,7 +91,13 @@ struct gr_attn_bwd_lds {
   static constexpr int BYTES = RING + (KV_LDS ? (BN / 32) * KVW : 0);
 };
 
-template <class T, int D, int BM, int BN, bool CAUSAL>
+// PRE (fp16 with scale log2(e) <= 1, K held in registers): K pre-scaled by
+// c = scale log2(e) (one more fp16 rounding, relative 2^-11) so that S comes
+// out in log2 units, and the S accumulators start from the queries' -L
+// log2(e): p = 2^S with no vector multiply-add per score. The dP
+// accumulators always start from -delta, so dS = p dP. Both statistics sit
+// negated in LDS and are read straight into the accumulators.
+template <class T, int D, int BM, int BN, bool CAUSAL, bool PRE = false>
 __global__ __launch_bounds__(BN / 32 * 64) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1)))
 void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
   typedef gr_mfma<T> MF;
@@ -142,6 +148,13 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
       vf[ds] = gr_as<vec8>(gr_ld16(V + (long long)(kw0 + l32) * a.sn + ds * 16 + 8 * g));
     }
   }
+  static_assert(!(PRE && KVL), "the K pre-scale needs K in registers");
+  if constexpr (PRE) {
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kf[ds][e] = (T)((float)kf[ds][e] * c);
+  }
   auto kfrag = [&](int ds) -> vec8 {
     if constexpr (KVL) return gr_as<vec8>(gr_ld16(kvs + l32 * (D * 2) + gr_swz<CPR>(l32, 2 * ds + g) * 16));
     else return kf[ds];
@@ -168,8 +181,8 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
     ql.load(dO + (long long)qt * BM * a.sn, s + L::QT);
     float* stat = reinterpret_cast<float*>(s + 2 * L::QT);
     const long long r0 = (long long)bh * a.N + (long long)qt * BM;
-    if (tid < BM) stat[tid] = a.lse[r0 + tid] * 1.4426950408889634f;
-    else if (tid < 2 * BM) stat[tid] = a.delta[r0 + tid - BM];
+    if (tid < BM) stat[tid] = a.lse[r0 + tid] * -1.4426950408889634f;
+    else if (tid < 2 * BM) stat[tid] = -a.delta[r0 + tid - BM];
   };
   load_tile(qt0, 0);
   __builtin_amdgcn_s_waitcnt(0);
@@ -181,15 +194,22 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
     if (qt + 1 < nqt) load_tile(qt + 1, st ^ 1);
     const char* qs = lds + st * L::STAGE;
     const char* dos = qs + L::QT;
-    const float* lse2 = reinterpret_cast<const float*>(qs + 2 * L::QT);
-    const float* dlt = lse2 + BM;
+    const float* nlse2 = reinterpret_cast<const float*>(qs + 2 * L::QT);   // -L log2(e)
+    const float* ndlt = nlse2 + BM;                                          // -delta
     const int q0 = qt * BM;
 
     vec8 pb[QJ][2], dsb[QJ][2];
 #pragma unroll
     for (int j = 0; j < QJ; ++j) {
-      // S and dP for queries j*32..+32 (row permuted) and this wave's keys
-      gr_f32x16 sa = (gr_f32x16)(0.f), dpa = (gr_f32x16)(0.f);
+      // S and dP for queries j*32..+32 (row permuted) and this wave's keys,
+      // from the queries' statistics (register r: query j*32 + 16(r/8) + 8g + r%8)
+      gr_f32x16 sa, dpa;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int ql_ = j * 32 + 16 * (r >> 3) + 8 * g + (r & 7);
+        sa[r] = PRE ? nlse2[ql_] : 0.f;
+        dpa[r] = ndlt[ql_];
+      }
       const int row = j * 32 + gr_perm32(l32);
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
@@ -217,9 +237,9 @@ void gr_attn_bwd_kernel(gr_attn_bwd_args a) {
           for (int u = 0; u < 2; ++u) {
             const int r = 8 * hf + e + u;
             const int ql_ = j * 32 + 16 * hf + 8 * g + e + u;
-            const float p = gr_exp2(sa[r] * c - lse2[ql_]);
+            const float p = PRE ? gr_exp2(sa[r]) : gr_exp2(fmaf(sa[r], c, nlse2[ql_]));
             p2[u] = p;
-            d2[u] = p * (dpa[r] - dlt[ql_]);
+            d2[u] = p * dpa[r];
           }
           pw[e >> 1] = gr_pack2f<T>(p2[0], p2[1]);
           dw[e >> 1] = gr_pack2f<T>(d2[0], d2[1]);
@@ -261,7 +281,12 @@ struct gr_attn_bwd_dq_lds {
 // per lane); key tiles of BN stream through LDS with their rows stored in the
 // gr_perm32 order, which makes each half-wave's S^T / dP^T accumulators 8
 // consecutive keys -- the B operand of dQ^T += K^T dS^T.
-template <class T, int D, int NW, int BN, bool CAUSAL>
+// PRE (fp16 with scale log2(e) <= 1): Q pre-scaled by c = scale log2(e) in
+// registers (one more fp16 rounding, relative 2^-11) so that S^T comes out in
+// log2 units, and the S^T accumulators start from -L log2(e): p = 2^S^T with
+// no vector multiply-add per score. The dP^T accumulators always start from
+// -delta, so dS = p dP^T.
+template <class T, int D, int NW, int BN, bool CAUSAL, bool PRE = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1)))
 void gr_attn_bwd_dq_kernel(gr_attn_bwd_args a) {
   typedef gr_mfma<T> MF;
@@ -314,6 +339,15 @@ void gr_attn_bwd_dq_kernel(gr_attn_bwd_args a) {
     dlt += gr_xor32(dlt);
     if (g == 0) a.delta[(long long)bh * a.N + myq] = dlt;
   }
+  if constexpr (PRE) {
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[ds][e] = (T)((float)qf[ds][e] * c);
+  }
+  // the accumulators' starting values: this lane's query's -L log2(e) (PRE)
+  // and -delta, the same in all 16 registers
+  const gr_f32x16 s_init = (gr_f32x16)(PRE ? -lse2 : 0.f), dp_init = (gr_f32x16)(-dlt);
   gr_f32x16 dqt[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) dqt[db] = (gr_f32x16)(0.f);
@@ -340,7 +374,7 @@ void gr_attn_bwd_dq_kernel(gr_attn_bwd_args a) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         // S^T and dP^T for keys kb*32.. (LDS rows kb*32 + l32) against this lane's query
-        gr_f32x16 sa = (gr_f32x16)(0.f), dpa = (gr_f32x16)(0.f);
+        gr_f32x16 sa = s_init, dpa = dp_init;
         const int row = kb * 32 + l32;
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
@@ -365,8 +399,8 @@ void gr_attn_bwd_dq_kernel(gr_attn_bwd_args a) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
               const int r = 8 * hf + e + u;
-              const float p = gr_exp2(sa[r] * c - lse2);
-              d2[u] = p * (dpa[r] - dlt);
+              const float p = PRE ? gr_exp2(sa[r]) : gr_exp2(fmaf(sa[r], c, -lse2));
+              d2[u] = p * dpa[r];
             }
             dw[e >> 1] = gr_pack2f<T>(d2[0], d2[1]);
           }
