@@ -528,7 +528,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--kernel", default="descent",
                     help="descent | handwritten | fp32 (only the fp32 configs through gr_attn_fwd) | hipblaslt-mlp "
-                         "(torch.matmul on the two C4 GEMMs, the library reference point) | PATH of a "
+                         "(torch.matmul on the two C4 GEMMs, the library reference point) | training (only the "
+                         "C2 and C3 training legs: forward with lse, backward, torch SDPA's backward) | PATH of a "
                          "saved module (.hip as RunLogger writes it, or a .json holding a program key): re-time "
                          "that module alone (reference bench.py --kernel)")
     ap.add_argument("--search-seconds", type=float, default=60.0, dest="search_seconds",
@@ -575,6 +576,9 @@ def main() -> int:
         return 0
     if args.kernel == "hipblaslt-mlp":
         print(json.dumps(hipblaslt_mlp(args.steps, args.warmup, args.seed)), flush=True)
+        return 0
+    if args.kernel == "training":
+        print(json.dumps(attention_training(args.steps, args.seed)), flush=True)
         return 0
     if args.kernel not in ("descent", "handwritten"):
         print(json.dumps(bench_module(args.kernel, args.steps, args.warmup, args.seed)), flush=True)
