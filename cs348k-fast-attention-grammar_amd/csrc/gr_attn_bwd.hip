@@ -64,6 +64,6 @@ extern "C" int gr_attn_bwd(const void* q, const void* k, const void* v, const vo
     return gr::fail(GR_E_ARG, "gr_attn_bwd: dtype %d unsupported (GR_F16 or GR_BF16)", dtype);
   if (D == 128) return gr_attn_bwd_launch_d128(a, dtype == GR_BF16, c, st);
   if (D != 64) return gr::fail(GR_E_ARG, "gr_attn_bwd: head dim D=%d unsupported (64 or 128)", D);
-  return dtype == GR_BF16 ? launch_bwd<__bf16, 64, 64, 128>(a, c, st) : launch_bwd<_Float16, 64, 64, 128>(a, c, st);
+  return dtype == GR_BF16 ? launch_bwd<__bf16, 64, 128, 128>(a, c, st) : launch_bwd<_Float16, 64, 128, 128>(a, c, st);
 }
 

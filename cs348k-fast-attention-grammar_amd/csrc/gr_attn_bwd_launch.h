@@ -16,12 +16,14 @@ bool bwd_prescale(const gr_attn_bwd_args& a) {
   return gr_is_same<T, _Float16>::value && a.scale * 1.4426950408889634f <= 1.0f;
 }
 
-// Backward tiles. dK/dV: (queries per tile, keys per workgroup) = (64, 128),
-// one wave per 32 keys. dQ: key tiles of 64, 8 waves (256 queries) per
-// workgroup when N allows it, else 4.
+// Backward tiles. dK/dV: (queries per tile, keys per workgroup) = (128, 128)
+// at d = 64, (64, 128) at d = 128, one wave per 32 keys. dQ: key tiles of 128
+// at d = 64, 64 at d = 128, 8 waves (256 queries) per workgroup when N allows
+// it, else 4. (At C2 the 128-deep tiles took dQ from 28.7 to 28.0 us and
+// dK/dV from 35.5 to 34.8 us: half the tile barriers and loads per MFMA.)
 template <class T, int D, int NW>
 void launch_bwd_dq(const gr_attn_bwd_args& a, bool causal, hipStream_t st) {
-  constexpr int DQ_BN = 64;
+  constexpr int DQ_BN = D <= 64 ? 128 : 64;
   const dim3 grid((unsigned)((long long)a.B * a.H * (a.N / (NW * 32))));
   constexpr int LDS = gr_attn_bwd_dq_lds<D, DQ_BN>::BYTES;
   const bool pre = bwd_prescale<T>(a);
