@@ -132,7 +132,9 @@ int gr_plan_time(gr_plan* p, void* stream, int warmup, int iters, int mode, floa
  *  128 (128 at D = 64 only), 0 = 128 at D = 64 when it divides N, else 64
  *  or 32. fp16 at D = 64, non-causal, 256 x 64 and N a multiple of 256 runs
  *  the kernel with two waves per SIMD and a hand-ordered main loop (160 KiB
- *  of LDS). */
+ *  of LDS); so does fp16 or bf16 at D = 128 with K transposed, causal or not,
+ *  at 256 x 64 and N a multiple of 256 (D = 128 is the default tile there).
+ *  Causal grids run each XCD's query blocks longest-first. */
 int gr_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int B, int H,
                 int N, int D, const long long* q_strides, const long long* k_strides,
                 const long long* v_strides, const long long* o_strides, int k_transposed,
