@@ -32,8 +32,8 @@ int launch_flash(const gr_attn_args& a, hipStream_t st) {
   return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_fwd launch");
 }
 
-// fp16, D = 64, non-causal, 256 x 64 tiles without the training forward's
-// log-sum-exp: two waves per SIMD with the hand-ordered main loop
+// fp16, D = 64, non-causal, 256 x 64 tiles (with or without the training
+// forward's log-sum-exp): two waves per SIMD with the hand-ordered main loop
 // (gr_flash_w2.h); N a multiple of 256.
 template <bool KT>
 int launch_w2(const gr_attn_args& a, hipStream_t st) {
@@ -57,13 +57,15 @@ int launch_w2h(const gr_attn_args& a, hipStream_t st) {
 // Tile configurations compiled into the library: (block_m, block_n) ->
 // (waves, query blocks per wave, key tile). One wave per 32 queries.
 // block_m 0 / block_n 0 pick the largest tiles that divide N (256 x 128 at
-// D = 64, 256 x 64 at D = 128).
+// D = 64, 256 x 64 at D = 128), except 256 x 64 where the two-wave body of
+// gr_flash_w2.h applies (fp16, D = 64, non-causal, N a multiple of 256).
 template <class T, int D, bool CAUSAL, bool KT>
 int dispatch_tiles(const gr_attn_args& a, int bm, int bn, hipStream_t st) {
   if (bm == 0) bm = a.N % 256 == 0 ? 256 : a.N % 128 == 0 ? 128 : 64;
-  if (bn == 0) bn = (D == 64 && a.N % 128 == 0) ? 128 : a.N % 64 == 0 ? 64 : 32;
-  if constexpr (gr_is_same<T, _Float16>::value && D == 64 && !CAUSAL)
-    if (bm == 256 && bn == 64 && a.lse == nullptr && a.N % 256 == 0) return launch_w2<KT>(a, st);
+  constexpr bool W2 = gr_is_same<T, _Float16>::value && D == 64 && !CAUSAL;
+  if (bn == 0) bn = (W2 && bm == 256 && a.N % 256 == 0) ? 64 : (D == 64 && a.N % 128 == 0) ? 128 : a.N % 64 == 0 ? 64 : 32;
+  if constexpr (W2)
+    if (bm == 256 && bn == 64 && a.N % 256 == 0 && a.Nq == a.N) return launch_w2<KT>(a, st);
   if constexpr (D == 128 && KT)
     if (bm == 256 && bn == 64 && a.lse == nullptr && a.N % 256 == 0 && a.Nq == a.N) return launch_w2h<T, CAUSAL>(a, st);
   if (bm == 256 && bn == 64) return launch_flash<T, D, 64, 8, 1, CAUSAL, KT>(a, st);

@@ -392,7 +392,12 @@ __device__ __forceinline__ void gr_flash_w2_body(const gr_attn_args& a, char* ld
   // O = O^T^T / l, staged through this wave's own Q area (no other wave
   // touches it) as whole 16-byte row chunks
   constexpr int CPR = D / 8;
-  const float inv = 1.0f / (lsum + gr_xor32(lsum));
+  const float lrow = lsum + gr_xor32(lsum);
+  const float inv = 1.0f / lrow;
+  // the training forward's row log-sum-exp (natural log): the base is -cinit
+  // in the pre-scaled (log2) units of the scores
+  if (a.lse && g == 0)
+    a.lse[(long long)bh * a.Nq + qw + l32] = (__builtin_amdgcn_logf(lrow) - cinit[0]) * 0.6931471805599453f;
   char* const stage = qarea;
 #pragma unroll
   for (int db = 0; db < 2; ++db)

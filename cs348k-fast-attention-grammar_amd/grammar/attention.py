@@ -21,11 +21,15 @@ def _strides3(t, dims=(0, 1, 2)) -> "ctypes.Array":
     return rt._ll3(*(int(t.stride(d)) for d in dims))
 
 
-def default_tiles(N: int, D: int) -> tuple:
-    """(block_m, block_n) that gr_attn_fwd picks for block_m = block_n = 0:
-    the largest query tile of 256 / 128 / 64 dividing N, and 128 keys per
-    tile at D = 64 when they divide N, else 64 or 32."""
+def default_tiles(N: int, D: int, dtype: str | None = None, causal: bool = False) -> tuple:
+    """(block_m, block_n) of the flash body's largest tiles: the largest query
+    tile of 256 / 128 / 64 dividing N, and 128 keys per tile at D = 64 when
+    they divide N, else 64 or 32. With the dtype given, what gr_attn_fwd
+    picks for block_m = block_n = 0: the same, except 256 x 64 where the
+    two-wave body applies (fp16, D = 64, non-causal, N a multiple of 256)."""
     bm = 256 if N % 256 == 0 else 128 if N % 128 == 0 else 64
+    if dtype == "fp16" and D == 64 and not causal and N % 256 == 0:
+        return bm, 64
     bn = 128 if (D == 64 and N % 128 == 0) else 64 if N % 64 == 0 else 32
     return bm, bn
 

@@ -130,7 +130,8 @@ int gr_plan_time(gr_plan* p, void* stream, int warmup, int iters, int mode, floa
  *  129 / 257: 128 / 256 with the software-pipelined schedule), 0 = the
  *  largest of 256 / 128 / 64 dividing N. block_n: keys per tile, 32 / 64 /
  *  128 (128 at D = 64 only), 0 = 128 at D = 64 when it divides N, else 64
- *  or 32. fp16 at D = 64, non-causal, 256 x 64 and N a multiple of 256 runs
+ *  or 32, but 64 where the two-wave body below applies at block_m 256.
+ *  fp16 at D = 64, non-causal, 256 x 64 and N a multiple of 256 runs
  *  the kernel with two waves per SIMD and a hand-ordered main loop (160 KiB
  *  of LDS); so does fp16 or bf16 at D = 128 with K transposed, causal or not,
  *  at 256 x 64 and N a multiple of 256 (D = 128 is the default tile there).

@@ -521,6 +521,9 @@ BWD = [
     (1, 2, 384, 64, "bf16", True),      # N not a multiple of 256: 4-wave dQ workgroups
     (1, 2, 640, 128, "fp16", False),
     (1, 2, 2048, 128, "bf16", True),
+    # fp16 d 64 non-causal, N a multiple of 256: the training forward (and its
+    # lse) on the two-wave body at the default tile, 16 key tiles
+    (1, 2, 1024, 64, "fp16", False),
 ]
 
 
