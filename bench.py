@@ -4,7 +4,7 @@ fp16 MFMA peak on one MI355X at B=4, H=16, N=1024, d=64 (BASELINE.json
 config C2), with the descent's evals/min measured in the same run.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2|C3]
-                    [--search-seconds S] [--kernel descent|handwritten|fp32|hipblaslt-mlp|PATH]
+                    [--search-seconds S] [--kernel descent|handwritten|fp32|hipblaslt-mlp|training|PATH]
 
 1. Descent: the stochastic rewrite descent runs from the naive 8-stage
    attention program (every stage its own kernel, full-extent tiles) for at
@@ -16,7 +16,8 @@ config C2), with the descent's evals/min measured in the same run.
    whole batch, inputs resident in HBM. W untimed warmup steps, then exactly
    K steps between two hipEvents recorded on the stream the kernels run on,
    after a device synchronize on both sides.
-3. Beside it: the hand-written gr_attn_fwd at its default tile, the C4 MLP
+3. Beside it: the hand-written gr_attn_fwd on the flash body's largest tile
+   (256 x 128 at d = 64; --block-m / --block-n pick others), the C4 MLP
    block through the two-GEMM gr_mlp_fwd, the committed descent-found programs
    for C3 (causal attention) and C4 (MLP), the training path (forward with
    row log-sum-exp, then dQ/dK/dV) at C2 and C3 beside torch SDPA, and the
