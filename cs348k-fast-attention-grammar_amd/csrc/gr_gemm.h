@@ -320,15 +320,17 @@ __device__ __forceinline__ void gr_mfma32_acc(gr_f32x16& acc, V a, V b) {
 // k tile -> ring depth of the one-wave body (LDS: two 64-deep or four 32-deep stages)
 template <int BK> struct gr_gemm_w4_stages { static constexpr int value = BK == 64 ? 2 : 4; };
 
-template <class T, bool B_KMAJOR, int EPI, int BK = 64>
+// BNT: the tile's columns, 256 (waves of 128 x 128) or 128 (waves of 128 x 64).
+template <class T, bool B_KMAJOR, int EPI, int BK = 64, int BNT = 256>
 __device__ __forceinline__ void gr_gemm_w4_body(const gr_gemm_args& a, char* lds) {
   typedef gr_mfma<T> MF;
   typedef typename MF::vec8 vec8;
-  constexpr int BM = 256, BN = 256, WGM = 2, WGN = 2, STAGES = gr_gemm_w4_stages<BK>::value;
+  constexpr int BM = 256, BN = BNT, WGM = 2, WGN = 2, STAGES = gr_gemm_w4_stages<BK>::value;
   typedef gr_gemm_cfg<BM, BN, BK, WGM, WGN, STAGES> G;
   constexpr int NT = G::NT, TM = G::TM, TN = G::TN, CPR = BK / 8, KS = BK / 16;
+  constexpr int NMF = TN * TM;                       // MFMAs per 16-deep k step
   constexpr int GROUP_M = 8;
-  static_assert(NT == 256 && TM == 4 && TN == 4, "four waves of 128 x 128");
+  static_assert(NT == 256 && TM == 4 && (TN == 4 || TN == 2), "four waves of 128 x 128 or 128 x 64");
   static_assert(BK == 32 || BK == 64, "32- or 64-deep k tiles");
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -361,14 +363,24 @@ __device__ __forceinline__ void gr_gemm_w4_body(const gr_gemm_args& a, char* lds
   for (int i = 0; i < TN; ++i)
 #pragma unroll
     for (int j = 0; j < TM; ++j) acc[i][j] = (gr_f32x16)(0.f);
+  // wait states between vector writes of the accumulators and the MFMAs that
+  // read them (or back): the compiler counts none into inline assembly
+  auto acc_guard = [&]() {
+    if constexpr (TN == 4)
+      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"
+                   : "+a"(acc[0][0]), "+a"(acc[0][1]), "+a"(acc[0][2]), "+a"(acc[0][3]), "+a"(acc[1][0]),
+                     "+a"(acc[1][1]), "+a"(acc[1][2]), "+a"(acc[1][3]), "+a"(acc[2][0]), "+a"(acc[2][1]),
+                     "+a"(acc[2][2]), "+a"(acc[2][3]), "+a"(acc[3][0]), "+a"(acc[3][1]), "+a"(acc[3][2]),
+                     "+a"(acc[3][3]));
+    else
+      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"
+                   : "+a"(acc[0][0]), "+a"(acc[0][1]), "+a"(acc[0][2]), "+a"(acc[0][3]), "+a"(acc[1][0]),
+                     "+a"(acc[1][1]), "+a"(acc[1][2]), "+a"(acc[1][3]));
+  };
   // the zeroing moves retire before the first MFMA reads them as its
-  // accumulator: the compiler counts no wait states into inline assembly,
-  // and without this the last-zeroed register of a block was read stale
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"
-               : "+a"(acc[0][0]), "+a"(acc[0][1]), "+a"(acc[0][2]), "+a"(acc[0][3]), "+a"(acc[1][0]),
-                 "+a"(acc[1][1]), "+a"(acc[1][2]), "+a"(acc[1][3]), "+a"(acc[2][0]), "+a"(acc[2][1]),
-                 "+a"(acc[2][2]), "+a"(acc[2][3]), "+a"(acc[3][0]), "+a"(acc[3][1]), "+a"(acc[3][2]),
-                 "+a"(acc[3][3]));
+  // accumulator (without this the last-zeroed register of a block was read
+  // stale)
+  acc_guard();
 
   const int nk = a.K / BK;
   typedef gr_lds_loader<T, BM, BK, NT> LA;
@@ -380,7 +392,8 @@ __device__ __forceinline__ void gr_gemm_w4_body(const gr_gemm_args& a, char* lds
   else lb.init(tid, a.b_s, BK, cols_ok / 8);
   constexpr int PER_A = LA::PER, PER_TILE = LA::PER + LB::PER;   // direct loads per thread and tile
   static_assert((BM * BK / 8) % NT == 0 && (BN * BK / 8) % NT == 0, "whole chunks per thread");
-  static_assert(PER_TILE <= 16 && (STAGES - 1) * PER_TILE < 64, "one load per MFMA slot; vmcnt range");
+  constexpr int LPS = (PER_TILE + NMF - 1) / NMF;   // direct loads per MFMA slot of a refilling k step
+  static_assert(LPS <= 2 && (STAGES - 1) * PER_TILE < 64, "at most two loads per MFMA slot; vmcnt range");
   auto stage = [&](int t) -> char* { return lds + (t % STAGES) * G::STAGE; };
   auto load_tile = [&](int t) {
     if (t < nk) {
@@ -418,24 +431,27 @@ __device__ __forceinline__ void gr_gemm_w4_body(const gr_gemm_args& a, char* lds
 #pragma unroll
   for (int j = 0; j < TM; ++j) am[0][j] = afrag(stage(0), 0, j);
 
-  // One k step: 16 MFMAs from fragment buffer CB. MORE: the next step's
+  // One k step: TN * TM MFMAs from fragment buffer CB. MORE: the next step's
   // fragments (from `nxt`, depth nks) into buffer 1 - CB, one read after each
-  // of the first eight MFMAs in the order of their first use (am[0], bt[0],
-  // am[1..3], bt[1..3]). LOAD: the direct loads of tile load_t, one after each MFMA.
+  // of the first TM + TN MFMAs in the order of their first use (am[0], bt[0],
+  // am[1..3], bt[1..TN-1]). LOAD: the direct loads of tile load_t, LPS after
+  // each MFMA.
   auto kstep = [&](auto cb_tag, auto more_tag, auto load_tag, const char* nxt, int nks, int load_t) {
     constexpr int CB = decltype(cb_tag)::value, NB = 1 - CB;
     constexpr bool MORE = decltype(more_tag)::value, LOAD = decltype(load_tag)::value;
 #pragma unroll
-    for (int idx = 0; idx < 16; ++idx) {
+    for (int idx = 0; idx < NMF; ++idx) {
       gr_mfma32_acc(acc[idx >> 2][idx & 3], bt[CB][idx >> 2], am[CB][idx & 3]);
       if constexpr (MORE) {
         if (idx == 0) am[NB][0] = afrag(nxt, nks, 0);
         else if (idx == 1) bt[NB][0] = bfrag(nxt, nks, 0);
         else if (idx < 5) am[NB][idx - 1] = afrag(nxt, nks, idx - 1);
-        else if (idx < 8) bt[NB][idx - 4] = bfrag(nxt, nks, idx - 4);
+        else if (idx < 4 + TN) bt[NB][idx - 4] = bfrag(nxt, nks, idx - 4);
       }
       if constexpr (LOAD) {
-        if (idx < PER_TILE) load_one(load_t, idx);
+#pragma unroll
+        for (int l = 0; l < LPS; ++l)
+          if (idx * LPS + l < PER_TILE) load_one(load_t, idx * LPS + l);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -470,25 +486,21 @@ __device__ __forceinline__ void gr_gemm_w4_body(const gr_gemm_args& a, char* lds
   // the MFMA results before any vector read of the accumulators (the compiler
   // does not count wait states after inline assembly), then every wave past
   // its operand reads before the output tile overwrites the stages
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3"
-               : "+a"(acc[0][0]), "+a"(acc[0][1]), "+a"(acc[0][2]), "+a"(acc[0][3]), "+a"(acc[1][0]),
-                 "+a"(acc[1][1]), "+a"(acc[1][2]), "+a"(acc[1][3]), "+a"(acc[2][0]), "+a"(acc[2][1]),
-                 "+a"(acc[2][2]), "+a"(acc[2][3]), "+a"(acc[3][0]), "+a"(acc[3][1]), "+a"(acc[3][2]),
-                 "+a"(acc[3][3]));
+  acc_guard();
   __syncthreads();
   gr_gemm_store_tile<T, BM, BN, TM, TN, NT, EPI>(a, acc, lds, wm * G::WM, wn * G::WN, tm, tn, z, rows_ok, cols_ok);
 }
 
 // LDS bytes of the one-wave body: the operand ring or the staged output tile
-template <int BK>
+template <int BK, int BNT = 256>
 struct gr_gemm_w4_lds {
-  typedef gr_gemm_cfg<256, 256, BK, 2, 2, gr_gemm_w4_stages<BK>::value> G;
+  typedef gr_gemm_cfg<256, BNT, BK, 2, 2, gr_gemm_w4_stages<BK>::value> G;
   static constexpr int value = G::LDS;
 };
 
-template <class T, bool B_KMAJOR, int EPI, int BK = 64>
+template <class T, bool B_KMAJOR, int EPI, int BK = 64, int BNT = 256>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
 void gr_gemm_w4_kernel(gr_gemm_args a) {
   extern __shared__ __attribute__((aligned(16))) char gr_lds[];
-  gr_gemm_w4_body<T, B_KMAJOR, EPI, BK>(a, gr_lds);
+  gr_gemm_w4_body<T, B_KMAJOR, EPI, BK, BNT>(a, gr_lds);
 }

@@ -24,15 +24,55 @@ int launch_gemm(const gr_gemm_args& a, int batch, hipStream_t st) {
   return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_gemm launch");
 }
 
+// Compute units of the current device (0 if unknown), read once per device.
+int cu_count() {
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cache[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 // The 256 x 256 tile: four waves (one per SIMD) of 128 x 128, the
-// hand-ordered main loop of gr_gemm_w4_body.
+// hand-ordered main loop of gr_gemm_w4_body, one workgroup per CU. When the
+// last round of workgroups would leave more than half of the CUs idle (X W1
+// of the C4 MLP: 1,376 tiles on 256 CUs, a sixth round of 96), the columns
+// past the whole rounds go to a second launch of the same body on 256 x 128
+// tiles (waves of 128 x 64), if those fit in one round: 1,280 + 192 there.
 template <class T, bool KM, int EPI, int BK>
 int launch_gemm_w4(const gr_gemm_args& a, int batch, hipStream_t st) {
   if (a.K % BK)
     return gr::fail(GR_E_ARG, "gr_gemm: K=%d must be a multiple of the k tile %d", a.K, BK);
-  const long long nblk = (long long)((a.M + 255) / 256) * ((a.N + 255) / 256);
+  const int mt = (a.M + 255) / 256, nt = (a.N + 255) / 256;
+  const long long nblk = (long long)mt * nt;
   if (nblk <= 0 || nblk > 0x7fffffffLL || batch > 65535)
     return gr::fail(GR_E_ARG, "gr_gemm: grid (%lld tiles, batch %d) out of range", nblk, batch);
+  const int cus = cu_count();
+  if (batch == 1 && cus > 0 && nblk > cus) {
+    const long long rounds = (nblk + cus - 1) / cus;
+    const long long last = nblk - (rounds - 1) * cus;            // workgroups of the last round
+    const int nt_main = (int)((rounds - 1) * cus / mt);          // column tiles of the whole rounds
+    const int col0 = nt_main * 256;
+    const long long rest = (long long)mt * ((a.N - col0 + 127) / 128);
+    if (2 * last <= cus && nt_main > 0 && nt_main < nt && rest <= cus) {
+      gr_gemm_args m = a, r = a;
+      m.N = col0;
+      r.N = a.N - col0;
+      r.b = static_cast<const T*>(a.b) + (KM ? (long long)col0 * a.b_s : (long long)col0);
+      r.c = static_cast<T*>(a.c) + col0;
+      if (a.r) r.r = static_cast<const T*>(a.r) + col0;
+      hipLaunchKernelGGL((gr_gemm_w4_kernel<T, KM, EPI, BK>), dim3((unsigned)((long long)mt * nt_main)), dim3(256),
+                         gr_gemm_w4_lds<BK>::value, st, m);
+      const int rc = gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_gemm launch");
+      if (rc) return rc;
+      hipLaunchKernelGGL((gr_gemm_w4_kernel<T, KM, EPI, BK, 128>), dim3((unsigned)rest), dim3(256),
+                         (gr_gemm_w4_lds<BK, 128>::value), st, r);
+      return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_gemm launch");
+    }
+  }
   hipLaunchKernelGGL((gr_gemm_w4_kernel<T, KM, EPI, BK>), dim3((unsigned)nblk, (unsigned)batch), dim3(256),
                      gr_gemm_w4_lds<BK>::value, st, a);
   return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_gemm launch");

@@ -63,6 +63,12 @@ CASES = [
     (1, 256, 256, 64, "bf16", "none", 1.0, False, (256, 256)),
     (1, 512, 512, 96, "fp16", "silu", 1.0, False, (256, 256)),
     (2, 256, 512, 192, "bf16", "relu", 0.5, True, (256, 256)),
+    # a last round of at most half the CUs (256 on MI355X): the columns past
+    # the whole rounds run as 256 x 128 tiles in a second launch (ragged in
+    # the second and third case: 320 columns there)
+    (1, 4096, 4352, 128, "fp16", "silu", 1.0, False, (256, 256)),
+    (1, 4096, 4416, 64, "bf16", "relu", 1.0, True, (256, 256)),
+    (1, 4096, 4416, 96, "fp16", "none", 0.5, False, (256, 256)),
 ]
 
 
