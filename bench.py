@@ -4,7 +4,7 @@ fp16 MFMA peak on one MI355X at B=4, H=16, N=1024, d=64 (BASELINE.json
 config C2), with the descent's evals/min measured in the same run.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2|C3]
-                    [--search-seconds S] [--kernel descent|handwritten|fp32|hipblaslt-mlp|training|PATH]
+                    [--search-seconds S] [--kernel descent|handwritten|fp32|hipblaslt-mlp|mlp|training|PATH]
 
 1. Descent: the stochastic rewrite descent runs from the naive 8-stage
    attention program (every stage its own kernel, full-extent tiles) for at
@@ -435,6 +435,26 @@ def hipblaslt_mlp(steps: int, warmup: int, seed: int) -> dict:
             "shapes": {"X": [C4.M, C4.Dm], "W1": [C4.Dm, C4.Hd], "W2": [C4.Hd, C4.Dm]}}
 
 
+def library_mlp(steps: int, warmup: int, seed: int) -> dict:
+    """The library's C4 MLP block (gr_mlp_fwd: X W1 + SiLU, then H W2, on the
+    one-wave 256 x 256 GEMM body) timed alone, as the default run's `mlp_c4`
+    leg times it, so that rocprofv3 has a committed command for its kernels."""
+    import torch
+    from grammar.gemm import mlp_fwd
+    from grammar.workloads import C4, mlp_inputs
+    dev = torch.device("cuda:0")
+    x, w1, w2 = mlp_inputs(C4, seed=seed, device=dev)
+    h = torch.empty((C4.M, C4.Hd), dtype=x.dtype, device=dev)
+    y = torch.empty((C4.M, C4.Dm), dtype=x.dtype, device=dev)
+    ms = timed(lambda: mlp_fwd(x, w1, w2, h=h, out=y), steps, warmup)
+    tflops = C4.flops / (ms * 1e-3) / 1e12
+    log(f"[bench] C4 MLP (gr_mlp_fwd): {ms:.4f} ms  {tflops:.1f} TFLOP/s")
+    return {"metric": "C4 MLP TFLOP/s, gr_mlp_fwd", "steps": steps, "warmup": warmup,
+            "ms_per_step": round(ms, 6), "tflops": round(tflops, 3),
+            "frac_of_peak": round(tflops / PEAK_TFLOPS["fp16"], 4),
+            "shapes": {"X": [C4.M, C4.Dm], "W1": [C4.Dm, C4.Hd], "W2": [C4.Hd, C4.Dm]}}
+
+
 def bench_module(path: str, steps: int, warmup: int, seed: int) -> dict:
     """Time one saved module -- a rendered .hip (it carries its launch plan
     and KERNEL_META) or a .json with a program key -- on seeded inputs,
@@ -529,7 +549,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--kernel", default="descent",
                     help="descent | handwritten | fp32 (only the fp32 configs through gr_attn_fwd) | hipblaslt-mlp "
-                         "(torch.matmul on the two C4 GEMMs, the library reference point) | training (only the "
+                         "(torch.matmul on the two C4 GEMMs, the library reference point) | mlp (the library's C4 MLP block, "
+                         "gr_mlp_fwd, alone) | training (only the "
                          "C2 and C3 training legs: forward with lse, backward, torch SDPA's backward) | PATH of a "
                          "saved module (.hip as RunLogger writes it, or a .json holding a program key): re-time "
                          "that module alone (reference bench.py --kernel)")
@@ -577,6 +598,9 @@ def main() -> int:
         return 0
     if args.kernel == "hipblaslt-mlp":
         print(json.dumps(hipblaslt_mlp(args.steps, args.warmup, args.seed)), flush=True)
+        return 0
+    if args.kernel == "mlp":
+        print(json.dumps(library_mlp(args.steps, args.warmup, args.seed)), flush=True)
         return 0
     if args.kernel == "training":
         print(json.dumps(attention_training(args.steps, args.seed)), flush=True)
