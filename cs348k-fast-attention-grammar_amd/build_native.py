@@ -42,8 +42,10 @@ COMMON = [
 # Per-source extra flags. The backward's d = 128 dK/dV kernel runs one wave
 # per SIMD; left to its heuristics the backend then puts every MFMA
 # accumulator in AGPRs and copies the score accumulators to VGPRs (and back)
-# for the softmax arithmetic on every tile. VGPR-form MFMAs need no copies and
-# fit in 245 VGPRs (the d = 64 kernels are faster with the heuristics).
+# for the softmax arithmetic on every tile. With VGPR-form MFMAs the score
+# accumulators stay in VGPRs, and the dK/dV accumulators, pinned to AGPRs by
+# inline assembly, need no copies either (the d = 64 kernels are faster with
+# the heuristics).
 EXTRA = {"gr_attn_bwd128.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 

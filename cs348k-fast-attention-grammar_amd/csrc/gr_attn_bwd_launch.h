@@ -16,11 +16,12 @@ bool bwd_prescale(const gr_attn_bwd_args& a) {
   return gr_is_same<T, _Float16>::value && a.scale * 1.4426950408889634f <= 1.0f;
 }
 
-// Backward tiles. dK/dV: (queries per tile, keys per workgroup) = (128, 128)
-// at d = 64, (64, 128) at d = 128, one wave per 32 keys. dQ: key tiles of 128
-// at d = 64, 64 at d = 128, 8 waves (256 queries) per workgroup when N allows
-// it, else 4. (At C2 the 128-deep tiles took dQ from 28.7 to 28.0 us and
-// dK/dV from 35.5 to 34.8 us: half the tile barriers and loads per MFMA.)
+// Backward tiles. dK/dV: (queries per tile, keys per workgroup) = (128, 128),
+// one wave per 32 keys. dQ: key tiles of 128 at d = 64, 64 at d = 128, 8 waves
+// (256 queries) per workgroup when N allows it, else 4. (At C2 the 128-deep
+// tiles took dQ from 28.7 to 28.0 us and dK/dV from 35.5 to 34.8 us: half the
+// tile barriers and loads per MFMA; at C3 the dK/dV kernel's 128-query tiles
+// ran 661 against 682 us for 64.)
 template <class T, int D, int NW>
 void launch_bwd_dq(const gr_attn_bwd_args& a, bool causal, hipStream_t st) {
   constexpr int DQ_BN = D <= 64 ? 128 : 64;
@@ -48,13 +49,19 @@ int launch_bwd(const gr_attn_bwd_args& a, bool causal, hipStream_t st) {
   if (rc) return rc;
   const dim3 grid((unsigned)((long long)a.B * a.H * (a.N / BN)));
   constexpr int LDS = gr_attn_bwd_lds<D, BM, BN>::BYTES;
-  constexpr bool CAN_PRE = !gr_attn_bwd_lds<D, BM, BN>::KV_LDS;   // K in registers
-  const bool pre = CAN_PRE && bwd_prescale<T>(a);
+  const bool pre = bwd_prescale<T>(a);
   const dim3 blk(BN / 32 * 64);
-  if (causal && pre) hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, true, CAN_PRE>), grid, blk, LDS, st, a);
-  else if (causal) hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, true, false>), grid, blk, LDS, st, a);
-  else if (pre) hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, false, CAN_PRE>), grid, blk, LDS, st, a);
-  else hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, false, false>), grid, blk, LDS, st, a);
+  if constexpr (D == 128) {
+    if (causal && pre) hipLaunchKernelGGL((gr_attn_bwd128_kernel<T, BM, BN, true, true>), grid, blk, LDS, st, a);
+    else if (causal) hipLaunchKernelGGL((gr_attn_bwd128_kernel<T, BM, BN, true, false>), grid, blk, LDS, st, a);
+    else if (pre) hipLaunchKernelGGL((gr_attn_bwd128_kernel<T, BM, BN, false, true>), grid, blk, LDS, st, a);
+    else hipLaunchKernelGGL((gr_attn_bwd128_kernel<T, BM, BN, false, false>), grid, blk, LDS, st, a);
+  } else {
+    if (causal && pre) hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, true, true>), grid, blk, LDS, st, a);
+    else if (causal) hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, true, false>), grid, blk, LDS, st, a);
+    else if (pre) hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, false, true>), grid, blk, LDS, st, a);
+    else hipLaunchKernelGGL((gr_attn_bwd_kernel<T, D, BM, BN, false, false>), grid, blk, LDS, st, a);
+  }
   return gr::hip_check(hipGetLastError(), GR_E_LAUNCH, "gr_attn_bwd dK/dV launch");
 }
 
