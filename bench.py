@@ -522,7 +522,7 @@ def bench_module(path: str, steps: int, warmup: int, seed: int) -> dict:
             "unit": "TFLOP/s", "ms_per_step": round(ms, 6), "steps": steps, "warmup": warmup,
             "clock_ramp_ms": CLOCK_RAMP_MS, "timing": "gr_plan_time batches (median of 3)",
             "flops": flops, "flops_exact": meta.get("flops_exact"),
-            "dtype": mod.plan["dtype"], "stages": len([st for st in mod.plan["steps"] if not st.get("merge")]),
+            "dtype": mod.plan["dtype"], "stages": len([st for st in mod.plan["steps"] if not (st.get("merge") or st.get("tail"))]),
             "lowering": [st["lowering"] for st in mod.plan["steps"]], "check": check}
 
 

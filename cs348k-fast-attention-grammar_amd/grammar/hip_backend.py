@@ -481,6 +481,35 @@ GEMM_WAVES_N = {32: 1, 64: 1, 128: 2, 256: 2}
 GEMM_TILE_WAVES = (4, 8)
 
 
+GEMM_CUS = 256                # compute units of the gfx950 parts this backend targets (MI355X, MI350X)
+
+
+def _gemm_w4_lds(bk, bnt=256):
+    """LDS bytes of the one-wave 256 x BNT body (gr_gemm_w4_lds): two
+    64-deep or four 32-deep operand stages, or the staged output tile."""
+    stages = 2 if bk == 64 else 4
+    return max(stages * (256 + bnt) * bk * 2, 256 * bnt * 2)
+
+
+def _gemm_w4_split(M, N, batch, cus=GEMM_CUS):
+    """The column split of a one-wave 256 x 256 GEMM launch whose last round
+    of workgroups would leave more than half of the CUs idle (the library's
+    launch_gemm_w4 rule): (col0, main tiles, 256 x 128 tail tiles) with the
+    columns from col0 on in the tail launch, or None."""
+    mt, nt = _cdiv(M, 256), _cdiv(N, 256)
+    nblk = mt * nt
+    if batch != 1 or nblk <= cus:
+        return None
+    rounds = _cdiv(nblk, cus)
+    last = nblk - (rounds - 1) * cus
+    nt_main = (rounds - 1) * cus // mt
+    col0 = nt_main * 256
+    rest = mt * _cdiv(N - col0, 128)
+    if 2 * last <= cus and 0 < nt_main < nt and rest <= cus:
+        return col0, mt * nt_main, rest
+    return None
+
+
 def _gemm_lds(bm, bn, bk):
     """LDS bytes of the GEMM kernel: two operand stages, or the staged output
     tile (gr_gemm_cfg::LDS)."""
@@ -744,26 +773,46 @@ void {kname}({params}) {{
                       "lds": _gemm_f32_lds(f["BM"], f["BN"], f["BK"], f["kmajor"]), "args": args,
                       "lowering": "gemm", "tiles": {"block_m": f["BM"], "block_n": f["BN"], "block_k": f["BK"]}}
     if f.get("W4"):
-        code = f"""
-// stage {loop.out}: MFMA GEMM {f['M']}x{f['N']}x{f['K']} (x{f['batch']}), tile 256x256x{f['BK']},
-// four waves of 128 x 128 (one per SIMD, hand-ordered main loop)
+        def w4_kernel(name, col0, ncols, bnt, what):
+            # columns col0 .. col0 + ncols of C (B, C and R offset by col0)
+            boff = f"{col0} * {f['K']}LL" if f["kmajor"] else f"{col0}LL"
+            rl = (f"\n  a.r = {_cname(f['res'])} + {col0}LL; a.r_sb = {f['c_sb']}LL; a.r_sm = {f['N']};"
+                  if f.get("res") else "")
+            return f"""
+// stage {loop.out}: MFMA GEMM {f['M']}x{f['N']}x{f['K']} (x{f['batch']}), {what},
+// four waves of 128 x {bnt // 2} (one per SIMD, hand-ordered main loop)
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1)))
-void {kname}({params}) {{
+void {name}({params}) {{
   extern __shared__ __attribute__((aligned(16))) char gr_gemm_smem[];
   gr_gemm_args a;
-  a.a = {_cname(f['a'])}; a.b = {_cname(f['b'])}; a.c = {_cname(f['c'])};
+  a.a = {_cname(f['a'])}; a.b = {_cname(f['b'])} + {boff}; a.c = {_cname(f['c'])} + {col0}LL;
   a.a_sb = {f['a_sb']}LL; a.a_sm = {f['K']};
   a.b_sb = {f['b_sb']}LL; a.b_s = {f['K'] if f['kmajor'] else f['N']};
   a.c_sb = {f['c_sb']}LL; a.c_sm = {f['N']};
-  a.M = {f['M']}; a.N = {f['N']}; a.K = {f['K']};
-  a.alpha = {_flt(f['alpha'])};{res_line}
-  gr_gemm_w4_body<{T}, {km}, {f['act']}, {f['BK']}>(a, gr_gemm_smem);
+  a.M = {f['M']}; a.N = {ncols}; a.K = {f['K']};
+  a.alpha = {_flt(f['alpha'])};{rl}
+  gr_gemm_w4_body<{T}, {km}, {f['act']}, {f['BK']}, {bnt}>(a, gr_gemm_smem);
 }}
 """
-        grid = -(-f["M"] // 256) * -(-f["N"] // 256)
-        return code, {"kernel": kname, "grid": [grid, f["batch"], 1], "block": [256, 1, 1],
-                      "lds": _gemm_lds(256, 256, f["BK"]), "args": args, "lowering": "gemm",
-                      "tiles": {"block_m": 256, "block_n": 256, "block_k": f["BK"], "waves": 4}}
+        tiles = {"block_m": 256, "block_n": 256, "block_k": f["BK"], "waves": 4}
+        split = _gemm_w4_split(f["M"], f["N"], f["batch"])
+        if split is None:
+            code = w4_kernel(kname, 0, f["N"], 256, f"tile 256x256x{f['BK']}")
+            grid = _cdiv(f["M"], 256) * _cdiv(f["N"], 256)
+            return code, {"kernel": kname, "grid": [grid, f["batch"], 1], "block": [256, 1, 1],
+                          "lds": _gemm_w4_lds(f["BK"]), "args": args, "lowering": "gemm", "tiles": tiles}
+        # a last round of at most half the CUs: the columns past the whole
+        # rounds go to a second launch of the body on 256 x 128 tiles
+        col0, nmain, ntail = split
+        tname = f"{_cname(loop.out)}_tail_kernel"
+        code = (w4_kernel(kname, 0, col0, 256, f"columns 0-{col0 - 1}, tile 256x256x{f['BK']}")
+                + w4_kernel(tname, col0, f["N"] - col0, 128,
+                            f"columns {col0}-{f['N'] - 1}, tile 256x128x{f['BK']}"))
+        return code, [{"kernel": kname, "grid": [nmain, 1, 1], "block": [256, 1, 1],
+                       "lds": _gemm_w4_lds(f["BK"]), "args": args, "lowering": "gemm", "tiles": tiles},
+                      {"kernel": tname, "grid": [ntail, 1, 1], "block": [256, 1, 1],
+                       "lds": _gemm_w4_lds(f["BK"], 128), "args": args, "lowering": "gemm", "tail": True,
+                       "tiles": {**tiles, "block_n": 128, "col0": col0}}]
     tpl = f"{T}, {f['BM']}, {f['BN']}, {f['BK']}, {f['WGM']}, {f['WGN']}, {km}, {f['act']}"
     nt = f["WGM"] * f["WGN"] * 64
     code = f"""

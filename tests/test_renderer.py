@@ -252,8 +252,8 @@ def test_gemm_waves_knob():
     steps = parse_plan(src0)["steps"]
     assert [s["block"] for s in steps] == [[256, 1, 1]] * 2 and [s["lds"] for s in steps] == [131072] * 2
     assert [s["tiles"]["waves"] for s in steps] == [4, 4]
-    assert "gr_gemm_w4_body<_Float16, false, 2, 64>(a, gr_gemm_smem);" in src0      # SiLU epilogue
-    assert "gr_gemm_w4_body<_Float16, false, 0, 64>(a, gr_gemm_smem);" in src0
+    assert "gr_gemm_w4_body<_Float16, false, 2, 64, 256>(a, gr_gemm_smem);" in src0      # SiLU epilogue
+    assert "gr_gemm_w4_body<_Float16, false, 0, 64, 256>(a, gr_gemm_smem);" in src0
     p.body[1].knobs["waves"] = 8
     assert structural_key(p) != key0
     src8 = emit_module(p)
@@ -266,6 +266,35 @@ def test_gemm_waves_knob():
     assert [schedule_knobs(s, q) for s in q.body] == [{}, {}]
     f = RM.build_mlp_ln(256, 512, 1024, tile=64)
     assert "waves" not in schedule_knobs(f.body[2], f)
+
+
+def test_gemm_stage_with_a_part_filled_last_round_splits_its_columns():
+    """A one-wave 256 x 256 GEMM stage whose last round of workgroups would
+    leave more than half of the 256 CUs idle (X W1 of the C4 MLP: 1,376
+    tiles, a sixth round of 96) renders two launches, as the library's
+    gr_gemm does: the first 10,240 columns on 256 x 256 tiles, the last 768
+    on 256 x 128 tiles with B, C (and R) offset by the first launch's
+    columns. H W2 (512 tiles, two whole rounds) stays one launch."""
+    import run_mlp_search as RM
+    from grammar import rewrites as R
+    from grammar import runtime as rt
+    from grammar.hip_backend import _gemm_w4_split
+    assert _gemm_w4_split(8192, 11008, 1) == (10240, 1280, 192)
+    assert _gemm_w4_split(8192, 4096, 1) is None                 # 512 tiles: whole rounds
+    assert _gemm_w4_split(8192, 11008, 2) is None                # batched launches stay whole
+    assert _gemm_w4_split(4096, 4416, 1) == (4096, 256, 48)      # ragged tail: 320 columns
+    p = RM.build_mlp_silu(8192, 4096, 11008, tile=256, subtile_k=64, dtype="fp16")
+    p = R.merge(p, p.body[0], p.body[1])
+    src = emit_module(p)
+    steps = parse_plan(src)["steps"]
+    assert [(s["kernel"], s["grid"][0], s["lds"], s.get("tail", False)) for s in steps] == [
+        ("t_a_kernel", 1280, 131072, False), ("t_a_tail_kernel", 192, 98304, True), ("t_y_kernel", 512, 131072, False)]
+    assert steps[1]["tiles"]["block_n"] == 128 and steps[1]["tiles"]["col0"] == 10240
+    assert "a.M = 8192; a.N = 10240; a.K = 4096;" in src and "a.M = 8192; a.N = 768; a.K = 4096;" in src
+    assert "a.b = t_W1 + 10240LL; a.c = t_a + 10240LL;" in src
+    assert "gr_gemm_w4_body<_Float16, false, 2, 64, 128>(a, gr_gemm_smem);" in src
+    code = rt.compile_source(src, "c4_split.hip")
+    assert code[:4] == b"\x7fELF"
 
 
 def test_fp32_gemm_split_k_knob():

@@ -381,6 +381,40 @@ def test_gemm_waves_knob_schedules_agree(dt):
         assert np.array_equal(runs[4][name], runs[8][name]), name
 
 
+@pytest.mark.parametrize("dt,H", [("fp16", 4352), ("bf16", 4416)])
+def test_gemm_stage_split_into_two_launches(dt, H):
+    """Y = SiLU(X W1) W2 with X W1 at 4096 x H x 128 on 256 x 256 tiles: a
+    second round of 16 or 18 workgroups, so the stage renders two launches
+    (the first 4,096 columns on 256 x 256 tiles, the rest on 256 x 128; at
+    H = 4,416 the last of those is ragged). The intermediate a and Y against
+    the float64 closed form on the same rounded inputs."""
+    dev = _cuda()
+    import run_mlp_search as RM
+    from grammar import rewrites as R
+    from grammar.hip_module import load_module
+    M, Dm = 4096, 128
+    p = RM.build_mlp_silu(M, Dm, H, tile=256, subtile_k=64, dtype=dt)
+    p = R.merge(p, p.body[0], p.body[1])
+    mod = load_module(emit_module(p))
+    steps = [(s["kernel"], s["grid"][0]) for s in mod.plan["steps"]]
+    assert steps[:2] == [("t_a_kernel", 256), ("t_a_tail_kernel", 16 * ((H - 4096 + 127) // 128))], steps
+    print(f"[case] split GEMM stage {dt} M={M} Dm={Dm} H={H}: {steps}", flush=True)
+    ins = RM.mlp_inputs(M, Dm, H, dt, seed=3, device=str(dev))
+    tensors = mod.run_with([ins[n] for n in mod.inputs])
+    torch.cuda.synchronize()
+    x, w1, w2 = (ins[n].double().cpu().numpy() for n in ("X", "W1", "W2"))
+    a_ref = O.silu(x @ w1)
+    mx, mn = O.errors(tensors["a"].float().cpu().numpy(), a_ref)
+    print(f"[split] {dt} a: max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)
+    assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL
+    tail = tensors["a"][:, 4096:].float().cpu().numpy()
+    assert np.isfinite(tail).all() and float(np.abs(tail - a_ref[:, 4096:]).max()) <= O.MAX_ABS_TOL
+    ref = O.mlp_silu(x, w1, w2, dtype=np.float64)
+    mx, mn = O.errors(tensors["y"].float().cpu().numpy(), ref)
+    print(f"[split] {dt} y: max-abs {mx:.2e} mean-abs {mn:.2e}", flush=True)
+    assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL
+
+
 @pytest.mark.parametrize("ks_a,ks_r", [(2, 4), (8, 8), (4, 1)])
 def test_fp32_split_k_gemm_stages(ks_a, ks_r):
     """fp32 GEMM stages with K split over workgroups (schedule knob ksplit):
