@@ -41,7 +41,9 @@ def test_committed_best_programs_rebuild():
         lowerings[name] = [s["lowering"] for s in parse_plan(emit_module(p))["steps"]]
     assert lowerings["attn_c2_best.json"] == ["flash"]
     assert lowerings["attn_c3_best.json"] == ["flash"]
-    assert lowerings["mlp_c4_best.json"] == ["gemm", "gemm"]
+    # X W1's 1,376 tiles leave a part-filled last round: its stage renders a
+    # second (tail) launch
+    assert lowerings["mlp_c4_best.json"] == ["gemm", "gemm", "gemm"]
 
 
 def test_save_best_round_trip(tmp_path):
