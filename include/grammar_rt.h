@@ -225,6 +225,10 @@ int gr_attn_decode_noalloc(const void* q, const void* k, const void* v, void* o,
  *  (0 = 256). Any M; N a multiple of 8; K a multiple of 32 (the square
  *  tiles use 64-deep k tiles when K allows). The 256 x 256 tile runs four
  *  waves of 128 x 128 (one per SIMD); the other tiles run eight waves.
+ *  With batch 1, a 256 x 256 launch whose last round of workgroups would
+ *  fill at most half of the device's CUs is issued as two launches on the
+ *  stream: the columns of the whole rounds, then the rest on 256 x 128
+ *  tiles (same results: each output's k order is unchanged).
  *  Edge tiles of C are stored only where valid. */
 #define GR_EPI_NONE 0
 #define GR_EPI_RELU 1
