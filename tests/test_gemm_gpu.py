@@ -91,6 +91,24 @@ def test_gemm_small_parity(case):
     _check(c, ref, f"gemm {case}")
 
 
+@pytest.mark.parametrize("dt,N,km", [("fp16", 4352, False), ("bf16", 4416, True)])
+def test_split_launch_matches_the_whole_grid(dt, N, km):
+    """A batch-1 launch whose last round is part-filled runs as two launches
+    (the tail on 256 x 128 tiles); a batch-2 launch of the same matrices
+    runs as one grid. Each output keeps its k order, so the two agree bit
+    for bit."""
+    dev = _cuda()
+    from grammar.gemm import gemm
+    print(f"[case] split vs whole grid {dt} M=4096 N={N} K=128 kmajor={km}", flush=True)
+    g = torch.Generator("cpu").manual_seed(21)
+    a = torch.randn((1, 4096, 128), generator=g).to(_td(dt)).to(dev)
+    b = (torch.randn((N, 128) if km else (128, N), generator=g) / np.sqrt(128)).to(_td(dt)).to(dev)
+    one = gemm(a, b, epilogue="silu", b_kmajor=km, block_m=256, block_n=256)
+    two = gemm(a.expand(2, -1, -1).contiguous(), b, epilogue="silu", b_kmajor=km, block_m=256, block_n=256)
+    torch.cuda.synchronize()
+    assert torch.equal(one[0], two[0]) and torch.equal(one[0], two[1])
+
+
 F32_CASES = [
     # batch, M, N, K, epilogue, alpha, b_kmajor, tile: the fp32 matrix-core GEMM (gr_gemm_f32.h)
     (1, 128, 128, 64, "none", 1.0, False, (64, 64)),
