@@ -556,6 +556,39 @@ def test_backward_parity(case):
         assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL, (name, mx, mn)
 
 
+@pytest.mark.parametrize("dt,causal", [("bf16", True), ("fp16", False)])
+def test_backward_full_length_d128_against_torch_fp32(dt, causal):
+    """dQ, dK, dV at N = 4,096, d = 128 (C3's length and head size, two heads)
+    against gradients that torch autograd takes through attention computed
+    in float32 on the GPU, from the same rounded inputs. At this length the
+    d = 128 dK/dV kernel runs 32 query tiles per key block (one masked, the
+    rest on the unmasked path). Bar: the attention bar on gradients scaled
+    to unit size."""
+    dev = _cuda()
+    from grammar.attention import flash_attention_bwd, flash_attention_fwd_train
+    B, H, N, D = 1, 2, 4096, 128
+    print(f"[case] backward B{B} H{H} N{N} d{D} {dt} causal={causal} against torch fp32", flush=True)
+    g = torch.Generator("cpu").manual_seed(29)
+    tdt = {"fp16": torch.float16, "bf16": torch.bfloat16}[dt]
+    q, k, v, do = (torch.randn((B, H, N, D), generator=g).to(tdt).to(dev) for _ in range(4))
+    o, lse = flash_attention_fwd_train(q, k, v, causal=causal)
+    dq, dk, dv = flash_attention_bwd(q, k, v, o, do, lse, causal=causal)
+    qf, kf, vf = (t.float().requires_grad_() for t in (q, k, v))
+    s = (qf @ kf.transpose(-1, -2).contiguous()) / math.sqrt(D)
+    if causal:
+        s = s.masked_fill(torch.ones(N, N, dtype=torch.bool, device=dev).triu(1), float("-inf"))
+    (torch.softmax(s, dim=-1) @ vf).backward(do.float())
+    torch.cuda.synchronize()
+    for name, got, ref in (("dq", dq, qf.grad), ("dk", dk, kf.grad), ("dv", dv, vf.grad)):
+        unit = max(1.0, float(ref.abs().max()))
+        d = (got.float() - ref).abs() / unit
+        mx, mn = float(d.max()), float(d.mean())
+        print(f"[parity] backward N{N} d{D} {dt} causal={causal} {name}: max-abs {mx:.3e} mean-abs {mn:.3e}",
+              flush=True)
+        assert torch.isfinite(got).all(), name
+        assert mx <= O.MAX_ABS_TOL and mn <= O.MEAN_ABS_TOL, (name, mx, mn)
+
+
 def test_bound_training_launchers_repeat_and_validate():
     """bind_flash_attention_train / bind_flash_attention_bwd: repeated launches
     give bit-identical results (no state carried between calls, delta is
